@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X dispatch library on BASELINE.json's metric.
+
+One step = one `c = a @ b` dispatch of BASELINE config 2 (bf16 x bf16 -> f32,
+M = N = K = 4096, N(0, 1/64) inputs resident in HBM, result into an HBM
+buffer) through vx_plugin_dispatch_async, exactly as a compiled Vx program
+issues it. `value` is whole-job TFLOP/s over the K timed steps.
+
+The same JSON line carries:
+  - roofline: the GEMM kernel's algorithmic FLOPs over its average duration
+    (hipEvents on the launch stream over the timed region) against the
+    MI355X dense bf16 MFMA peak, and its HBM traffic per launch from the
+    committed rocprofv3 PMC summary when one exists;
+  - cpu_baseline: the CPU oracle's bf16 -> f32 GEMM (the reference's
+    outlined-loop semantics, one thread) timed on a bounded block of rows of
+    the same GEMM;
+  - extra: flash-attention forward (config 3), int8 GEMV (config 5, weights
+    rotated through more than the 256 MB MALL) and int8 greedy decode
+    (config 4) when their paths are built.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only gemm,fa,gemv,decode]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters, committed
+    as profiles/<name>_traffic.json; None when not measured."""
+    p = ROOT / "profiles" / f"{name}_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
+    from vx_amd import abi
+    from vx_amd.abi import f32_to_bf16
+    from vx_amd.runtime import DeviceArray, matmul
+
+    rng = np.random.default_rng(2024)
+    a16 = f32_to_bf16(rng.normal(0, 1 / 64, (n, n)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1 / 64, (n, n)).astype(np.float32))
+    da, db = DeviceArray.of(lib, a16, abi.DTYPE_BF16), DeviceArray.of(lib, b16, abi.DTYPE_BF16)
+    dc = DeviceArray(lib, (n, n), abi.DTYPE_F32)
+    ad, bd, cd = da.descriptor(), db.descriptor(), dc.descriptor()
+    args = abi.CallArgs()
+    args.memref(ad, abi.DTYPE_BF16).scalar(0, abi.KIND_I64).memref(bd, abi.DTYPE_BF16)
+    args.scalar(1, abi.KIND_I64).scalar(0.0, abi.KIND_F32).memref(cd, abi.DTYPE_F32)
+    import ctypes
+    pl = abi.matmul_payload(outkind="buffer")
+    buf = ctypes.create_string_buffer(pl, len(pl))
+    argv, tags, nargs = args.arrays()
+    dispatch = lib.lib.vx_plugin_dispatch_async
+
+    before = lib.stats()
+    for _ in range(warmup):
+        dispatch(buf, len(pl), argv, tags, nargs)
+    timer.sync()
+    e0, e1 = timer.event(), timer.event()
+    t0 = time.perf_counter()
+    timer.record(e0)
+    for _ in range(steps):
+        dispatch(buf, len(pl), argv, tags, nargs)
+    timer.record(e1)
+    ms_events = timer.elapsed_ms(e0, e1)
+    timer.sync()
+    wall = time.perf_counter() - t0
+    after = lib.stats()
+    assert after["gemm_mfma"] - before["gemm_mfma"] == steps + warmup, "GEMM did not take the MFMA path"
+    c = dc.numpy()
+    assert np.isfinite(c).all()
+    for x in (da, db, dc):
+        x.free()
+    flops = 2.0 * n * n * n
+    ms_step = ms_events / steps
+    return dict(n=n, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / steps,
+                tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16)
+
+
+def bench_fa(lib, timer, steps: int, warmup: int):
+    from vx_amd import abi
+    from vx_amd.abi import f32_to_bf16
+    from vx_amd.runtime import DeviceArray, flash_attention_fwd
+
+    b, h, s, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(7)
+    arrs = [DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((b, h, s, d)).astype(np.float32)),
+                           abi.DTYPE_BF16) for _ in range(3)]
+    do = DeviceArray(lib, (b, h, s, d), abi.DTYPE_BF16)
+    dl = DeviceArray(lib, (b, h, s), abi.DTYPE_F32)
+    q, k, v = (x.ptr for x in arrs)
+
+    def call():
+        rc = flash_attention_fwd(lib, q, k, v, do.ptr, dl.ptr, b, h, h, s, s, d, 1.0 / np.sqrt(d), True)
+        assert rc == 0
+
+    for _ in range(warmup):
+        call()
+    timer.sync()
+    e0, e1 = timer.event(), timer.event()
+    timer.record(e0)
+    for _ in range(steps):
+        call()
+    timer.record(e1)
+    ms = timer.elapsed_ms(e0, e1) / steps
+    for x in arrs + [do, dl]:
+        x.free()
+    flops = 2.0 * b * h * s * s * d  # causal: half of 4*B*H*S^2*D
+    return dict(config="causal [4,32,2048,128] bf16", ms=ms, tflops=flops / (ms * 1e-3) / 1e12,
+                frac_of_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS)
+
+
+def bench_gemv(lib, timer, steps: int, warmup: int):
+    from vx_amd import abi
+    from vx_amd.abi import f32_to_bf16
+    from vx_amd.runtime import DeviceArray, gemv_i8
+
+    out = []
+    rng = np.random.default_rng(11)
+    for rows, cols in ((4096, 4096), (11008, 4096), (4096, 11008)):
+        wbytes = rows * cols
+        copies = max(6, -(-512 * 2**20 // wbytes))  # > 2x the 256 MB MALL
+        w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+        ws = [DeviceArray.of(lib, w, abi.DTYPE_I8) for _ in range(copies)]
+        sc = DeviceArray.of(lib, rng.uniform(0.001, 0.01, rows).astype(np.float32), abi.DTYPE_F32)
+        for batch in (1, 4, 16):
+            x = DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32)),
+                               abi.DTYPE_BF16)
+            y = DeviceArray(lib, (batch, rows), abi.DTYPE_F32)
+            n_calls = max(steps, copies)
+            for i in range(warmup):
+                gemv_i8(lib, ws[i % copies].ptr, sc.ptr, x.ptr, y.ptr, rows, cols, batch)
+            timer.sync()
+            e0, e1 = timer.event(), timer.event()
+            timer.record(e0)
+            for i in range(n_calls):
+                rc = gemv_i8(lib, ws[i % copies].ptr, sc.ptr, x.ptr, y.ptr, rows, cols, batch)
+                assert rc == 0
+            timer.record(e1)
+            ms = timer.elapsed_ms(e0, e1) / n_calls
+            nbytes = rows * cols + 4 * rows + 2 * batch * cols + 4 * batch * rows
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append(dict(shape=[rows, cols], batch=batch, us=ms * 1e3, gbs=gbs,
+                            frac_of_hbm=gbs / PEAK_HBM_GBS, rotated_copies=copies))
+            x.free()
+            y.free()
+        for a in ws + [sc]:
+            a.free()
+    return out
+
+
+def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
+    """The CPU oracle's bf16 -> f32 GEMM (one thread) on a block of rows of
+    the same 4096^3 GEMM, sized to about `budget_s` of work."""
+    import oracle
+
+    n = a16.shape[0]
+    t0 = time.perf_counter()
+    oracle.gemm_bf16_f32(a16, b16, rows=slice(0, 2))
+    per_row = (time.perf_counter() - t0) / 2
+    rows = int(max(2, min(n, budget_s / max(per_row, 1e-6))))
+    t0 = time.perf_counter()
+    oracle.gemm_bf16_f32(a16, b16, rows=slice(0, rows))
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * n * n
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="port",
+                sample=f"rows 0..{rows} of the {n}^3 bf16->f32 GEMM ({flops / 1e9:.1f} GFLOP in "
+                       f"{dt:.1f} s), oracle/vx_oracle.c loop nest, 1 thread")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", default="gemm,fa,gemv,decode")
+    ns = ap.parse_args()
+    if ns.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (its sharding is a "
+              "design in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+    only = set(ns.only.split(","))
+
+    from vx_amd.runtime import DispatchLibrary, HipTimer
+
+    lib = DispatchLibrary()
+    if lib.device_count() < 1:
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    timer = HipTimer()
+
+    log(f"gemm bf16->f32 4096^3: warmup {ns.warmup}, steps {ns.steps}")
+    g = bench_gemm(lib, timer, ns.steps, ns.warmup)
+    log(f"gemm {g['tflops']:.1f} TFLOP/s ({g['ms_per_step'] * 1e3:.1f} us/step)")
+
+    extra = {}
+    if "fa" in only:
+        log("flash attention config 3")
+        extra["flash_attn_fwd"] = bench_fa(lib, timer, max(5, ns.steps // 5), 2)
+        log(f"fa {extra['flash_attn_fwd']['tflops']:.1f} TFLOP/s")
+    if "gemv" in only:
+        log("int8 gemv config 5")
+        extra["gemv_i8"] = bench_gemv(lib, timer, max(20, ns.steps), 3)
+        log("gemv " + ", ".join(f"{r['shape'][0]}x{r['shape'][1]}b{r['batch']}:{r['gbs']:.0f}GB/s"
+                                for r in extra["gemv_i8"]))
+    if "decode" in only:
+        try:
+            from vx_amd import decode as _decode  # noqa: F401
+        except ImportError:
+            pass
+        else:
+            log("int8 decode config 4")
+            extra["decode_i8"] = _decode.bench(lib, timer)
+
+    cpu = None
+    if not ns.skip_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline_gemm(g["a16"], g["b16"])
+        cpu["nproc"] = os.cpu_count()
+
+    achieved = g["tflops"]
+    line = {
+        "metric": "GEMM & flash-attn fwd TFLOP/s (% MI355X bf16 peak); int8 decode tok/s bs=1",
+        "value": round(g["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": ns.steps,
+        "warmup": ns.warmup,
+        "ms_per_step": round(g["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "bf16 x bf16 -> f32 GEMM, M=N=K=4096 (BASELINE config 2), "
+                               "operands resident in HBM, one vx_plugin_dispatch_async per step",
+                   "m": 4096, "n": 4096, "k": 4096},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_from_profiles("gemm_bf16_4096")},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

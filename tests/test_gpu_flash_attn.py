@@ -1,0 +1,116 @@
+"""The flash-attention forward op on the GPU against the CPU oracle (f64
+two-pass softmax), including the full BASELINE config on sampled rows."""
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import announce
+from tests.parity import BF16_ABS, assert_max_abs
+from vx_amd import abi
+from vx_amd.abi import bf16_to_f32, f32_to_bf16
+from vx_amd.runtime import DeviceArray, flash_attention_fwd
+
+pytestmark = pytest.mark.gpu
+
+
+def run(lib, q16, k16, v16, heads, kv_heads, scale, causal, with_lse=True):
+    b, _, sq, d = q16.shape
+    sk = k16.shape[2]
+    dq = DeviceArray.of(lib, q16, abi.DTYPE_BF16)
+    dk = DeviceArray.of(lib, k16, abi.DTYPE_BF16)
+    dv = DeviceArray.of(lib, v16, abi.DTYPE_BF16)
+    do = DeviceArray(lib, q16.shape, abi.DTYPE_BF16)
+    dl = DeviceArray(lib, (b, heads, sq), abi.DTYPE_F32) if with_lse else None
+    rc = flash_attention_fwd(lib, dq.ptr, dk.ptr, dv.ptr, do.ptr, dl.ptr if dl else None, b, heads,
+                             kv_heads, sq, sk, d, scale, causal)
+    assert rc == 0
+    o = bf16_to_f32(do.numpy())
+    lse = dl.numpy() if dl else None
+    for a in (dq, dk, dv, do) + ((dl,) if dl else ()):
+        a.free()
+    return o, lse
+
+
+def randn16(rng, shape):
+    return f32_to_bf16(rng.standard_normal(shape).astype(np.float32))
+
+
+CASES = [
+    # batch, heads, kv_heads, seq_q, seq_k, head_dim
+    (1, 2, 2, 128, 128, 128),
+    (2, 4, 2, 200, 200, 64),
+    (1, 2, 1, 64, 300, 128),
+    (1, 1, 1, 1, 1, 128),
+    (1, 3, 3, 129, 129, 64),
+    (2, 2, 2, 300, 70, 128),
+]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("case", CASES)
+def test_matches_oracle(hiplib, case, causal, rng):
+    announce(f"flash attn {case} causal={causal}")
+    b, h, hk, sq, sk, d = case
+    q16, k16, v16 = randn16(rng, (b, h, sq, d)), randn16(rng, (b, hk, sk, d)), randn16(rng, (b, hk, sk, d))
+    scale = 1.0 / np.sqrt(d)
+    o, lse = run(hiplib, q16, k16, v16, h, hk, scale, causal)
+    rows = oracle.attention_all_rows(b, h, sq)
+    wo, wl = oracle.attention_rows(q16, k16, v16, h, hk, scale, causal, rows)
+    assert_max_abs(o.reshape(-1, d), wo, BF16_ABS, f"o {case}")
+    fin = np.isfinite(wl)
+    assert np.array_equal(np.isfinite(lse.ravel()), fin)
+    assert_max_abs(lse.ravel()[fin], wl[fin], 1e-3, f"lse {case}")
+    assert np.all(o.reshape(-1, d)[~fin] == 0)
+
+
+def test_closed_forms(hiplib, rng):
+    announce("flash attn closed forms")
+    b, h, s, d = 1, 4, 256, 128
+    k16, v16 = randn16(rng, (b, h, s, d)), randn16(rng, (b, h, s, d))
+    q16 = randn16(rng, (b, h, s, d))
+    o, lse = run(hiplib, q16, k16, v16, h, h, 0.125, True)
+    v = bf16_to_f32(v16)
+    # causal row 0 is V[0] (rounded once to bf16)
+    assert np.array_equal(o[:, :, 0], bf16_to_f32(f32_to_bf16(v[:, :, 0])))
+    # zero queries: prefix mean of V, lse = ln(count)
+    o0, l0 = run(hiplib, np.zeros_like(q16), k16, v16, h, h, 0.125, True)
+    prefix = np.cumsum(v.astype(np.float64), axis=2) / np.arange(1, s + 1)[None, None, :, None]
+    assert_max_abs(o0, prefix, 1e-2, "prefix mean")
+    assert_max_abs(l0, np.broadcast_to(np.log(np.arange(1, s + 1)), l0.shape), 1e-4, "ln count")
+
+
+def test_baseline_config_sampled(hiplib):
+    """[4, 32, 2048, 128] causal, N(0,1), scale 1/sqrt(128).
+    Rows sampled across batches, heads and block boundaries."""
+    announce("flash attn config 3")
+    rng = np.random.default_rng(7)
+    b, h, s, d = 4, 32, 2048, 128
+    q16, k16, v16 = (randn16(rng, (b, h, s, d)) for _ in range(3))
+    scale = 1.0 / np.sqrt(d)
+    o, lse = run(hiplib, q16, k16, v16, h, h, scale, True)
+    picks = [0, 1, 31, 32, 63, 64, 127, 128, 129, 1000, 1023, 1024, 2046, 2047]
+    rows = np.array([(bi, hi, qi) for bi in range(b) for hi in (0, 13, 31) for qi in picks],
+                    np.int64)
+    wo, wl = oracle.attention_rows(q16, k16, v16, h, h, scale, True, rows)
+    got = o[rows[:, 0], rows[:, 1], rows[:, 2]]
+    assert_max_abs(got, wo, BF16_ABS, "config 3 rows")
+    assert_max_abs(lse[rows[:, 0], rows[:, 1], rows[:, 2]], wl, 1e-3, "config 3 lse")
+    assert np.isfinite(o).all()
+
+
+def test_no_lse_and_refusals(hiplib, rng):
+    announce("flash attn refusals")
+    q16 = randn16(rng, (1, 2, 64, 64))
+    o, lse = run(hiplib, q16, q16, q16, 2, 2, 0.125, False, with_lse=False)
+    assert lse is None and np.isfinite(o).all()
+    dq = DeviceArray.of(hiplib, q16, abi.DTYPE_BF16)
+    p = dq.ptr
+    # head_dim 96 is not a kernel shape
+    assert flash_attention_fwd(hiplib, p, p, p, p, None, 1, 2, 2, 64, 64, 96, 0.125, False) == -4
+    # 3 heads cannot share 2 kv heads
+    assert flash_attention_fwd(hiplib, p, p, p, p, None, 1, 3, 2, 64, 64, 64, 0.125, False) == -1
+    # host memory is refused
+    assert flash_attention_fwd(hiplib, q16.ctypes.data, p, p, p, None, 1, 2, 2, 64, 64, 64, 0.125,
+                               False) == -3
+    dq.free()

@@ -1,0 +1,89 @@
+"""The int8 weight-only GEMV op on the GPU against the CPU oracle."""
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import announce
+from tests.parity import GEMV_REL, assert_rel
+from vx_amd import abi
+from vx_amd.abi import f32_to_bf16
+from vx_amd.runtime import DeviceArray, gemv_i8
+
+pytestmark = pytest.mark.gpu
+
+
+def run(lib, w, s, x16):
+    rows, cols = w.shape
+    batch = x16.shape[0]
+    dw = DeviceArray.of(lib, w, abi.DTYPE_I8)
+    ds = DeviceArray.of(lib, s, abi.DTYPE_F32)
+    dx = DeviceArray.of(lib, x16, abi.DTYPE_BF16)
+    dy = DeviceArray(lib, (batch, rows), abi.DTYPE_F32)
+    rc = gemv_i8(lib, dw.ptr, ds.ptr, dx.ptr, dy.ptr, rows, cols, batch)
+    assert rc == 0
+    y = dy.numpy()
+    for a in (dw, ds, dx, dy):
+        a.free()
+    return y
+
+
+def inputs(rng, rows, cols, batch):
+    w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+    s = rng.uniform(0.001, 0.01, rows).astype(np.float32)
+    x16 = f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32))
+    return w, s, x16
+
+
+@pytest.mark.parametrize("shape", [(4096, 4096), (11008, 4096), (4096, 11008)])
+@pytest.mark.parametrize("batch", [1, 4, 16])
+def test_llama7b_shapes(hiplib, shape, batch):
+    """Llama-2-7B linear shapes, batch 1/4/16."""
+    announce(f"gemv {shape} batch {batch}")
+    rng = np.random.default_rng(hash((shape, batch)) % 2**32)
+    w, s, x16 = inputs(rng, *shape, batch)
+    y = run(hiplib, w, s, x16)
+    assert_rel(y, oracle.gemv_i8_f64(w, s, x16), GEMV_REL, f"gemv {shape} b{batch}")
+    # the f32 oracle sums in another order; both sit near the f64 value
+    assert_rel(y, oracle.gemv_i8(w, s, x16), 2 * GEMV_REL, "vs f32 oracle")
+
+
+@pytest.mark.parametrize("shape,batch", [((7, 16), 1), ((33, 48), 3), ((1000, 2064), 5),
+                                         ((64, 4096), 16), ((1, 32), 2), ((9, 3000 + 8), 7)])
+def test_ragged(hiplib, shape, batch, rng):
+    announce(f"gemv ragged {shape} batch {batch}")
+    rows, cols = shape
+    if cols % 16:
+        cols += 16 - cols % 16
+    w, s, x16 = inputs(rng, rows, cols, batch)
+    y = run(hiplib, w, s, x16)
+    assert_rel(y, oracle.gemv_i8_f64(w, s, x16), GEMV_REL, f"gemv {shape}")
+
+
+def test_exact_integers(hiplib, rng):
+    """Integer activations: every partial sum is exact in f32 whatever the
+    order, so the GPU must equal scale * (exact dot) bit for bit."""
+    announce("gemv exact integers")
+    w = rng.integers(-127, 128, (4096, 11008), dtype=np.int8)
+    x = rng.integers(-8, 9, (4, 11008)).astype(np.float32)
+    s = rng.uniform(0.001, 0.01, 4096).astype(np.float32)
+    y = run(hiplib, w, s, f32_to_bf16(x))
+    exact = (w.astype(np.float64) @ x.astype(np.float64).T).T
+    assert np.array_equal(y, s[None, :] * exact.astype(np.float32))
+    assert np.array_equal(y, oracle.gemv_i8(w, s, f32_to_bf16(x)))
+
+
+def test_refusals(hiplib, rng):
+    announce("gemv refusals")
+    w, s, x16 = inputs(rng, 16, 32, 1)
+    dw = DeviceArray.of(hiplib, w, abi.DTYPE_I8)
+    ds = DeviceArray.of(hiplib, s, abi.DTYPE_F32)
+    dx = DeviceArray.of(hiplib, x16, abi.DTYPE_BF16)
+    dy = DeviceArray(hiplib, (1, 16), abi.DTYPE_F32)
+    assert gemv_i8(hiplib, dw.ptr, ds.ptr, dx.ptr, dy.ptr, 16, 24, 1) == -4  # cols % 16
+    assert gemv_i8(hiplib, dw.ptr, ds.ptr, dx.ptr, dy.ptr, 16, 32, 17) == -1  # batch
+    assert gemv_i8(hiplib, dw.ptr, ds.ptr, dx.ptr, dy.ptr, 0, 32, 1) == -1
+    assert gemv_i8(hiplib, w.ctypes.data, ds.ptr, dx.ptr, dy.ptr, 16, 32, 1) == -3  # host w
+    assert gemv_i8(hiplib, 0, ds.ptr, dx.ptr, dy.ptr, 16, 32, 1) == -1
+    for a in (dw, ds, dx, dy):
+        a.free()

@@ -1,0 +1,26 @@
+"""Builds and runs the GPU-free C++ unit tests of the vendor-free headers
+(tests/native/*.cpp), as the reference's runtime tests are built and run
+(reference tests/integration_test/runtime_test_build.rs: -Wall -Werror, and
+ASan/UBSan on request)."""
+
+import os
+import subprocess
+from pathlib import Path
+
+import pytest
+
+HERE = Path(__file__).resolve().parent
+NATIVE = HERE / "native"
+
+
+@pytest.mark.parametrize("src", sorted(p.name for p in NATIVE.glob("*_test.cpp")))
+@pytest.mark.parametrize("sanitize", [False, True])
+def test_native(src, sanitize, tmp_path):
+    exe = tmp_path / src.replace(".cpp", "")
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Werror", str(NATIVE / src), "-o", str(exe)]
+    if sanitize:
+        cmd[1:1] = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer"]
+    subprocess.run(cmd, check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    assert res.stdout.strip() == "ok"

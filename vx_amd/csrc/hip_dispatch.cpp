@@ -1,0 +1,829 @@
+/*
+ * hip_dispatch.cpp -- libvx_hip_dispatch.so, the vx_plugin_* ABI on one or
+ * more MI355X GPUs (gfx950).
+ *
+ * A drop-in for the CUDA dispatch library (reference
+ * runtime/cuda_dispatch.cpp): a compiled Vx program links it through
+ * VX_DISPATCH_LIB (reference src/jit.rs:235-265) and calls the entry points of
+ * include/vx_hardware_runtime.h. What differs is below the ABI:
+ *
+ *  - a routed `a @ b` (kind=matmul) runs on hand-written gfx950 kernels
+ *    (kernels/gemm.hip): no vendor BLAS;
+ *  - the mixed plan (bf16/f16 inputs, f32 result) the reference sends to the
+ *    host loop nest is routed to the GPU too;
+ *  - operands already in HBM are used in place; host operands are staged
+ *    through an exact-size pool (vx_device_pool_hip.h);
+ *  - everything else runs as the outlined host kernel, with HBM views copied
+ *    out and back (vx_host_fallback.h), because the compiler emits no AMDGPU
+ *    image yet;
+ *  - flash attention and the int8 GEMV are library ops (include/vx_hip_ops.h).
+ *
+ * Streams: each thread launches on its caller stream (vx_cuda_set_stream;
+ * default the null stream), as the reference does (:205-207). A launch
+ * returns at once; waits happen at read-backs, awaits and VX_CTRL_WAIT*.
+ *
+ * Environment: VX_DISPATCH_VERBOSE (routing narrative on stderr),
+ * VX_TIME_KERNEL (device time of each routed GEMM on stderr), VX_HIP_SYNC=1
+ * (wait after every launch, so a fault names its launch), VX_HIP_POOL_MAX_MB.
+ */
+#include "../../include/vx_hardware_runtime.h"
+#include "../../include/vx_hip_ops.h"
+#include "vx_device_pool_hip.h"
+#include "vx_dispatch_plan.h"
+#include "vx_hip_common.h"
+#include "vx_host_fallback.h"
+#include "vx_kernels.h"
+#include "vx_ops_internal.h"
+
+#include <atomic>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace {
+
+bool verbose() {
+  static const bool on = [] {
+    const char *v = getenv("VX_DISPATCH_VERBOSE");
+    return v && *v && strcmp(v, "0") != 0;
+  }();
+  return on;
+}
+
+bool sync_each_launch() {
+  static const bool on = [] {
+    const char *v = getenv("VX_HIP_SYNC");
+    return v && *v && strcmp(v, "0") != 0;
+  }();
+  return on;
+}
+
+bool hip_available() {
+  static const bool ok = [] {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) {
+      (void)hipGetLastError();
+      fprintf(stderr,
+              "[Vx HIP] no HIP device (%s); kernels will run on the host\n",
+              e == hipSuccess ? "none present" : hipGetErrorString(e));
+      return false;
+    }
+    return true;
+  }();
+  return ok;
+}
+
+thread_local hipStream_t caller_stream = nullptr;
+
+/* Declared ids the program said stand for a built-in device
+ * (VX_CTRL_LOCAL_DEVICE). Entries are written before the count that
+ * publishes them (reference runtime/cuda_dispatch.cpp:632-655). */
+struct LocalDevice {
+  int32_t declared;
+  int32_t builtin;
+};
+LocalDevice local_devices[64];
+std::atomic<size_t> local_device_count{0};
+std::mutex local_devices_mutex;
+
+int gpu_index(int32_t topology_id) {
+  const size_t n = local_device_count.load(std::memory_order_acquire);
+  for (size_t i = 0; i < n; ++i) {
+    if (local_devices[i].declared == topology_id) {
+      topology_id = local_devices[i].builtin;
+      break;
+    }
+  }
+  return vx_topology_device_index(topology_id, VX_TOPO_GPU_BASE);
+}
+
+/* Make the GPU `topology_id` names current. A non-GPU or absent id leaves the
+ * current device alone; a GPU this machine lacks is fatal (reference
+ * runtime/cuda_dispatch.cpp:707-729). */
+void select_device(int32_t topology_id, const char *why) {
+  const int index = gpu_index(topology_id);
+  if (index < 0) {
+    return;
+  }
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || index >= count) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: launch targets GPU %d, but this machine has %d\n",
+            index, count);
+    abort();
+  }
+  VX_HIP_CHECK(hipSetDevice(index));
+  if (verbose()) {
+    fprintf(stderr, "[Vx HIP] device %d %s\n", index, why);
+  }
+}
+
+/* True for memory the GPU owns (hipMalloc'd). Host memory, registered or not,
+ * answers false. */
+bool is_device_ptr(const void *p) {
+  if (!p || !hip_available()) {
+    return false;
+  }
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice;
+}
+
+void *device_malloc(size_t bytes) {
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return p;
+}
+
+void device_release(void *p, size_t) { (void)hipFree(p); }
+
+using Pool = vx::HipDevicePool<void *(*)(size_t), void (*)(void *, size_t)>;
+Pool &pool() {
+  static Pool *p =
+      new Pool(&device_malloc, &device_release, vx::hip_pool_cap_from_env());
+  return *p;
+}
+
+void wait_for_kernels(const char *why) {
+  if (verbose()) {
+    fprintf(stderr, "[Vx HIP] wait: %s\n", why);
+  }
+  hipError_t e = caller_stream ? hipStreamSynchronize(caller_stream)
+                               : hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    fprintf(stderr, "[Vx HIP] FATAL: a GPU launch failed (%s) before %s\n",
+            hipGetErrorString(e), why);
+    abort();
+  }
+}
+
+void started_kernel(const char *what) {
+  if (sync_each_launch()) {
+    wait_for_kernels(what);
+  }
+}
+
+/* Counters a test reads to prove which path ran (VX_HIP_CTRL_STATS). */
+std::atomic<int64_t> stat_gemm_device{0};
+std::atomic<int64_t> stat_gemm_mfma{0};
+std::atomic<int64_t> stat_gemm_tiled{0};
+std::atomic<int64_t> stat_host_fallback{0};
+std::atomic<int64_t> stat_staged_bytes{0};
+std::atomic<int> forced_gemm_kernel{0};
+
+/* An operand on the device: used in place, or a pooled packed copy. */
+struct DeviceOperand {
+  void *ptr = nullptr;
+  int64_t row_stride = 0;
+  size_t bytes = 0;
+  bool pooled = false;
+  ~DeviceOperand() {
+    if (pooled && ptr) {
+      /* The copy may still be read by a launch on the caller stream. */
+      wait_for_kernels("a staging buffer went back to the pool");
+      pool().release(ptr, bytes);
+    }
+  }
+};
+
+void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
+           size_t esz, DeviceOperand &out) {
+  if (is_device_ptr(data)) {
+    out.ptr = const_cast<void *>(data);
+    out.row_stride = row_stride;
+    return;
+  }
+  const size_t width = (size_t)cols * esz;
+  out.bytes = (size_t)rows * width;
+  out.ptr = pool().acquire(out.bytes);
+  if (!out.ptr) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: out of device memory staging %zu bytes "
+            "(%lld x %lld)\n",
+            out.bytes, (long long)rows, (long long)cols);
+    abort();
+  }
+  out.pooled = true;
+  out.row_stride = cols;
+  stat_staged_bytes += (int64_t)out.bytes;
+  VX_HIP_CHECK(hipMemcpy2DAsync(out.ptr, width, data, (size_t)row_stride * esz,
+                                width, (size_t)rows, hipMemcpyHostToDevice,
+                                caller_stream));
+}
+
+bool run_gemm(const vx_gemm_plan &plan) {
+  const size_t in_esz = vx_dtype_bytes(plan.dtype);
+  const size_t out_esz = vx_dtype_bytes(plan.out_dtype);
+  if (!in_esz || !out_esz) {
+    return false;
+  }
+  if (verbose()) {
+    fprintf(stderr, "[Vx HIP] GEMM %lldx%lldx%lld %s -> %s %s\n",
+            (long long)plan.m, (long long)plan.n, (long long)plan.k,
+            vx_dtype_name(plan.dtype), vx_dtype_name(plan.out_dtype),
+            plan.out_kind == VX_GEMM_OUT_SLOT ? "slot" : "buffer");
+  }
+
+  DeviceOperand a, b, c;
+  stage(plan.a_data, plan.m, plan.k, plan.a_row_stride, in_esz, a);
+  stage(plan.b_data, plan.k, plan.n, plan.b_row_stride, in_esz, b);
+  const bool out_is_device =
+      plan.out_kind == VX_GEMM_OUT_BUFFER && is_device_ptr(plan.out_data);
+  if (out_is_device) {
+    c.ptr = plan.out_data;
+    c.row_stride = plan.out_row_stride;
+  } else {
+    c.bytes = (size_t)plan.m * (size_t)plan.n * out_esz;
+    c.ptr = pool().acquire(c.bytes);
+    if (!c.ptr) {
+      fprintf(stderr, "[Vx HIP] FATAL: out of device memory for a %lldx%lld "
+                      "GEMM result\n",
+              (long long)plan.m, (long long)plan.n);
+      abort();
+    }
+    c.pooled = true;
+    c.row_stride = plan.n;
+  }
+
+  vxk::GemmArgs g;
+  g.in_dtype = plan.dtype;
+  g.out_dtype = plan.out_dtype;
+  g.m = plan.m, g.n = plan.n, g.k = plan.k;
+  g.a = a.ptr, g.b = b.ptr, g.c = c.ptr;
+  g.lda = a.row_stride, g.ldb = b.row_stride, g.ldc = c.row_stride;
+
+  vxk::GemmKernel which = vxk::gemm_pick(g);
+  const int forced = forced_gemm_kernel.load();
+  if (forced == vxk::GEMM_MFMA_256 || forced == vxk::GEMM_TILED) {
+    which = (vxk::GemmKernel)forced;
+  }
+
+  const bool time_kernel = getenv("VX_TIME_KERNEL") != nullptr;
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  if (time_kernel) {
+    VX_HIP_CHECK(hipEventCreate(&t0));
+    VX_HIP_CHECK(hipEventCreate(&t1));
+    VX_HIP_CHECK(hipEventRecord(t0, caller_stream));
+  }
+  if (!vxk::gemm_launch_kernel(which, g, caller_stream)) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: no GPU kernel takes the GEMM %lldx%lldx%lld %s -> "
+            "%s (strides %lld/%lld/%lld)\n",
+            (long long)g.m, (long long)g.n, (long long)g.k,
+            vx_dtype_name(g.in_dtype), vx_dtype_name(g.out_dtype),
+            (long long)g.lda, (long long)g.ldb, (long long)g.ldc);
+    abort();
+  }
+  if (time_kernel) {
+    VX_HIP_CHECK(hipEventRecord(t1, caller_stream));
+    VX_HIP_CHECK(hipEventSynchronize(t1));
+    float ms = 0.0f;
+    VX_HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
+    fprintf(stderr, "[Vx HIP] GEMM device time %.3f ms (%lldx%lldx%lld)\n", ms,
+            (long long)g.m, (long long)g.n, (long long)g.k);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+  }
+  ++stat_gemm_device;
+  (which == vxk::GEMM_MFMA_256 ? stat_gemm_mfma : stat_gemm_tiled)++;
+  started_kernel("a GEMM");
+
+  if (out_is_device) {
+    return true;
+  }
+  wait_for_kernels("a GEMM result was copied to host memory");
+  const size_t width = (size_t)plan.n * out_esz;
+  if (plan.out_kind == VX_GEMM_OUT_SLOT) {
+    /* The program frees a slot result with free(): it must be malloc memory
+     * (reference docs/lang/abi.md section 3.1). */
+    void *result = malloc((size_t)plan.m * width);
+    if (!result) {
+      fprintf(stderr, "[Vx HIP] FATAL: out of memory for a %lldx%lld result\n",
+              (long long)plan.m, (long long)plan.n);
+      abort();
+    }
+    VX_HIP_CHECK(hipMemcpy(result, c.ptr, (size_t)plan.m * width,
+                           hipMemcpyDeviceToHost));
+    vx_gemm_publish_slot(&plan, result);
+    return true;
+  }
+  VX_HIP_CHECK(hipMemcpy2D(plan.out_data, (size_t)plan.out_row_stride * out_esz,
+                           c.ptr, width, width, (size_t)plan.m,
+                           hipMemcpyDeviceToHost));
+  return true;
+}
+
+vx::HostCopies host_copies() {
+  vx::HostCopies io;
+  io.is_device = [](const void *p) { return is_device_ptr(p); };
+  io.to_host = [](void *dst, const void *src, size_t n) {
+    wait_for_kernels("a host kernel read GPU memory");
+    VX_HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+  };
+  io.to_device = [](void *dst, const void *src, size_t n) {
+    VX_HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+  };
+  return io;
+}
+
+void run_on_host(const void *payload, size_t payload_size, void **device_args,
+                 const int32_t *arg_tags, int64_t num_args) {
+  const char *name = static_cast<const char *>(payload);
+  if (vx_payload_field(payload, payload_size, "coop=")) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: %s is a cooperative kernel -- its barriers are "
+            "inside the thread loop, so no serial order of that loop computes "
+            "it, and this library has no device image for it\n",
+            name);
+    abort();
+  }
+  void *kernel = vx::host_kernel_symbol(name);
+  if (!kernel) {
+    fprintf(stderr, "[Vx HIP] FATAL: outlined kernel %s not found\n", name);
+    abort();
+  }
+  if (verbose()) {
+    const char *kind = vx_payload_field(payload, payload_size, "kind=");
+    fprintf(stderr, "[Vx HIP] %s (kind=%s) runs on the host\n", name,
+            kind ? kind : "<unclassified>");
+  }
+  ++stat_host_fallback;
+  if (!vx::call_on_host(kernel, device_args, arg_tags, num_args,
+                        host_copies())) {
+    fprintf(stderr, "[Vx HIP] FATAL: could not build a call for %s\n", name);
+    abort();
+  }
+}
+
+/* Arrival counts kept per (site, topology, stream), reference
+ * runtime/vx_arrival_counts.h semantics: take gives back a kept count of at
+ * least `bytes`; give keeps the larger of two and hands back the other. */
+class ArrivalCounts {
+public:
+  void *take(const void *site, uint32_t topo, const void *stream,
+             size_t bytes) {
+    std::lock_guard<std::mutex> hold(mu_);
+    auto it = kept_.find(Key{site, topo, stream});
+    if (it == kept_.end() || it->second.second < bytes) {
+      return nullptr;
+    }
+    void *count = it->second.first;
+    kept_.erase(it);
+    return count;
+  }
+  void *give(const void *site, uint32_t topo, const void *stream, void *count,
+             size_t bytes) {
+    std::lock_guard<std::mutex> hold(mu_);
+    Key key{site, topo, stream};
+    auto it = kept_.find(key);
+    if (it == kept_.end()) {
+      kept_.emplace(key, std::make_pair(count, bytes));
+      return nullptr;
+    }
+    if (it->second.second >= bytes) {
+      return count;
+    }
+    void *smaller = it->second.first;
+    it->second = std::make_pair(count, bytes);
+    return smaller;
+  }
+
+private:
+  using Key = std::tuple<const void *, uint32_t, const void *>;
+  std::mutex mu_;
+  std::map<Key, std::pair<void *, size_t>> kept_;
+};
+
+ArrivalCounts &arrival_counts() {
+  static ArrivalCounts *c = new ArrivalCounts();
+  return *c;
+}
+
+/* One-rank job state (reference runtime/vx_collective.h:288-330). */
+int32_t one_rank_ranks = 0;
+
+void collective_fatal(const char *why) {
+  fprintf(stderr, "[Vx HIP] FATAL: %s\n", why);
+  abort();
+}
+
+void one_rank_copy(const void *in, void *out, int64_t count, size_t esz,
+                   const char *name) {
+  char msg[256];
+  if (!one_rank_ranks) {
+    snprintf(msg, sizeof(msg), "%s ran before vx_collective_init.", name);
+    collective_fatal(msg);
+  }
+  if (count < 0) {
+    snprintf(msg, sizeof(msg), "%s got a count of %lld.", name,
+             (long long)count);
+    collective_fatal(msg);
+  }
+  if (in == out || count == 0) {
+    return;
+  }
+  const size_t bytes = (size_t)count * esz;
+  if (is_device_ptr(in) || is_device_ptr(out)) {
+    VX_HIP_CHECK(hipMemcpyAsync(out, in, bytes, hipMemcpyDefault,
+                                caller_stream));
+    started_kernel(name);
+  } else {
+    memmove(out, in, bytes);
+  }
+}
+
+} // namespace
+
+/* Used by the library ops (ops.cpp). */
+namespace vxops {
+hipStream_t stream() { return caller_stream; }
+bool device_present() { return hip_available(); }
+bool on_device(const void *p) { return is_device_ptr(p); }
+void launched(const char *what) { started_kernel(what); }
+bool chatty() { return verbose(); }
+} // namespace vxops
+
+extern "C" {
+
+void *vx_plugin_alloc_and_transfer(size_t bytes, void *host_ptr,
+                                   uint32_t topology_id,
+                                   uint32_t space_access) {
+  if (!hip_available() || gpu_index((int32_t)topology_id) < 0) {
+    void *p = malloc(bytes ? bytes : 1);
+    if (p && host_ptr && bytes) {
+      memcpy(p, host_ptr, bytes);
+    }
+    return p;
+  }
+  select_device((int32_t)topology_id, "stage");
+  if (space_access == VX_SPACE_ACCESS_HOST_READABLE) {
+    /* The model says the host may read this space; HBM is not host memory
+     * (reference runtime/cuda_dispatch.cpp:1172-1197). */
+    const char *strict = getenv("VX_STRICT_SPACES");
+    fprintf(stderr,
+            "[Vx HIP] %s: topology %u is declared host-readable, but its %zu "
+            "bytes are GPU memory the host cannot read\n",
+            strict ? "FATAL" : "WARNING", topology_id, bytes);
+    if (strict) {
+      abort();
+    }
+  }
+  void *p = nullptr;
+  VX_HIP_CHECK(hipMalloc(&p, bytes ? bytes : 1));
+  if (host_ptr && bytes) {
+    if (caller_stream) {
+      VX_HIP_CHECK(hipMemcpyAsync(p, host_ptr, bytes, hipMemcpyHostToDevice,
+                                  caller_stream));
+      VX_HIP_CHECK(hipStreamSynchronize(caller_stream));
+    } else {
+      VX_HIP_CHECK(hipMemcpy(p, host_ptr, bytes, hipMemcpyHostToDevice));
+    }
+  }
+  return p;
+}
+
+/* The copy ends before this returns, which the asynchronous contract allows:
+ * "a device may still copy". */
+void *vx_plugin_alloc_and_transfer_async(size_t bytes, void *host_ptr,
+                                         uint32_t topology_id,
+                                         uint32_t space_access) {
+  return vx_plugin_alloc_and_transfer(bytes, host_ptr, topology_id,
+                                      space_access);
+}
+
+uint64_t vx_plugin_dispatch_async(const void *binary_payload,
+                                  size_t payload_size, void **device_args,
+                                  const int32_t *arg_tags, int64_t num_args) {
+  const int32_t abi = vx_payload_abi(binary_payload, payload_size);
+  if (abi > VX_PAYLOAD_ABI) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: %s carries payload format abi=%d; this library "
+            "reads formats up to %d\n",
+            static_cast<const char *>(binary_payload), abi, VX_PAYLOAD_ABI);
+    abort();
+  }
+  vx_gemm_plan plan;
+  if (hip_available() &&
+      vx_gemm_plan_decode(binary_payload, payload_size, device_args, arg_tags,
+                          num_args, &plan)) {
+    select_device(vx_payload_topology(binary_payload, payload_size),
+                  "dispatch");
+    if (run_gemm(plan)) {
+      return 1;
+    }
+  }
+  run_on_host(binary_payload, payload_size, device_args, arg_tags, num_args);
+  return 1;
+}
+
+uint64_t vx_plugin_dispatch_async_flat(float *xout, float *x, float *w, int n,
+                                       int d) {
+  if (n <= 0 || d <= 0) {
+    return 1;
+  }
+  if (!hip_available()) {
+    /* No device: the plain loop the ABI documents (reference
+     * runtime/host_dispatch_common.h:648-660). */
+    for (int i = 0; i < d; ++i) {
+      float acc = 0.0f;
+      for (int j = 0; j < n; ++j) {
+        acc += w[(size_t)i * n + j] * x[j];
+      }
+      xout[i] = acc;
+    }
+    return 1;
+  }
+  /* xout[d] = W[d,n] x[n] is a GEMM with m = d, k = n, N = 1. */
+  DeviceOperand dw, dx, dy;
+  stage(w, d, n, n, sizeof(float), dw);
+  stage(x, n, 1, 1, sizeof(float), dx);
+  const bool out_is_device = is_device_ptr(xout);
+  if (out_is_device) {
+    dy.ptr = xout;
+  } else {
+    dy.bytes = (size_t)d * sizeof(float);
+    dy.ptr = pool().acquire(dy.bytes);
+    dy.pooled = true;
+  }
+  vxk::GemmArgs g;
+  g.in_dtype = g.out_dtype = VX_DTYPE_F32;
+  g.m = d, g.n = 1, g.k = n;
+  g.a = dw.ptr, g.b = dx.ptr, g.c = dy.ptr;
+  g.lda = dw.row_stride, g.ldb = 1, g.ldc = 1;
+  if (!vxk::gemm_launch(g, caller_stream)) {
+    fprintf(stderr, "[Vx HIP] FATAL: no GPU kernel takes a %dx%d matvec\n", d,
+            n);
+    abort();
+  }
+  started_kernel("a matrix-vector product");
+  if (!out_is_device) {
+    wait_for_kernels("a matrix-vector product was copied to host memory");
+    VX_HIP_CHECK(hipMemcpy(xout, dy.ptr, (size_t)d * sizeof(float),
+                           hipMemcpyDeviceToHost));
+  }
+  return 1;
+}
+
+void vx_plugin_await_future(uint64_t future_id) {
+  (void)future_id;
+  if (hip_available()) {
+    wait_for_kernels("a future was awaited");
+  }
+}
+
+int32_t vx_plugin_transfer_device_to_host(void *device_ptr, void *host_ptr,
+                                          size_t bytes, uint32_t topology_id) {
+  if (is_device_ptr(device_ptr)) {
+    select_device((int32_t)topology_id, "fetch");
+    wait_for_kernels("a tensor was copied to host memory");
+    VX_HIP_CHECK(hipMemcpy(host_ptr, device_ptr, bytes, hipMemcpyDeviceToHost));
+  } else if (bytes) {
+    memcpy(host_ptr, device_ptr, bytes);
+  }
+  return 1;
+}
+
+void *vx_plugin_transfer_peer(void *src_device_ptr, uint32_t src_topology_id,
+                              uint32_t dst_topology_id, size_t bytes) {
+  if (!is_device_ptr(src_device_ptr)) {
+    void *dst = malloc(bytes ? bytes : 1);
+    if (dst && src_device_ptr && bytes) {
+      memcpy(dst, src_device_ptr, bytes);
+    }
+    return dst;
+  }
+  const int src = gpu_index((int32_t)src_topology_id);
+  const int dst = gpu_index((int32_t)dst_topology_id);
+  if (src < 0 || dst < 0) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: peer transfer between topologies %u and %u, "
+            "which are not both GPUs\n",
+            src_topology_id, dst_topology_id);
+    abort();
+  }
+  select_device((int32_t)dst_topology_id, "peer");
+  void *p = nullptr;
+  VX_HIP_CHECK(hipMalloc(&p, bytes ? bytes : 1));
+  if (bytes) {
+    if (src == dst) {
+      VX_HIP_CHECK(hipMemcpyAsync(p, src_device_ptr, bytes,
+                                  hipMemcpyDeviceToDevice, caller_stream));
+    } else {
+      VX_HIP_CHECK(hipMemcpyPeerAsync(p, dst, src_device_ptr, src, bytes,
+                                      caller_stream));
+    }
+    started_kernel("a peer copy");
+  }
+  if (verbose()) {
+    fprintf(stderr, "[Vx HIP] peer %d -> %d, %zu bytes\n", src, dst, bytes);
+  }
+  return p;
+}
+
+void vx_plugin_free(void *device_ptr, uint32_t topology_id) {
+  if (!device_ptr) {
+    return;
+  }
+  if (is_device_ptr(device_ptr)) {
+    select_device((int32_t)topology_id, "free");
+    /* A launch still reading the buffer must end first. */
+    wait_for_kernels("a device buffer was freed");
+    VX_HIP_CHECK(hipFree(device_ptr));
+  } else {
+    free(device_ptr);
+  }
+}
+
+void *vx_plugin_arrivals_take(const void *site, size_t bytes, void *zeros,
+                              uint32_t topology_id, uint32_t space_access) {
+  if (void *kept = arrival_counts().take(site, topology_id, caller_stream,
+                                         bytes)) {
+    return kept;
+  }
+  return vx_plugin_alloc_and_transfer(bytes, zeros, topology_id, space_access);
+}
+
+void vx_plugin_arrivals_give(const void *site, void *count, size_t bytes,
+                             uint32_t topology_id) {
+  void *spare =
+      arrival_counts().give(site, topology_id, caller_stream, count, bytes);
+  if (spare) {
+    vx_plugin_free(spare, topology_id);
+  }
+}
+
+void vx_plugin_release_future(uint64_t future_id) { (void)future_id; }
+
+/* Vendor opcodes of this library (VX_CTRL_VENDOR_BASE and up). */
+#define VX_HIP_CTRL_GEMM_KERNEL (VX_CTRL_VENDOR_BASE + 1)
+#define VX_HIP_CTRL_STATS (VX_CTRL_VENDOR_BASE + 2)
+#define VX_HIP_CTRL_POOL_DRAIN (VX_CTRL_VENDOR_BASE + 3)
+
+int32_t vx_plugin_control(uint32_t opcode, void *payload) {
+  switch (opcode) {
+  case VX_CTRL_GET_DEVICE_COUNT: {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    return n;
+  }
+  case VX_CTRL_INIT_DEVICE:
+    return hip_available() ? 1 : 0;
+  case VX_CTRL_WAIT:
+  case VX_CTRL_WAIT_FOR_TENSORS:
+  case VX_CTRL_WAIT_FOR_THREAD:
+    if (hip_available()) {
+      wait_for_kernels("a read of GPU memory in place");
+    }
+    return 1;
+  case VX_CTRL_SHUTDOWN:
+    if (hip_available()) {
+      wait_for_kernels("shutdown");
+      pool().drain();
+    }
+    return 1;
+  case VX_CTRL_LOCAL_DEVICE: {
+    const int32_t *pair = static_cast<const int32_t *>(payload);
+    if (!pair) {
+      return 0;
+    }
+    std::lock_guard<std::mutex> hold(local_devices_mutex);
+    const size_t n = local_device_count.load(std::memory_order_relaxed);
+    for (size_t i = 0; i < n; ++i) {
+      if (local_devices[i].declared != pair[0]) {
+        continue;
+      }
+      if (local_devices[i].builtin != pair[1]) {
+        fprintf(stderr,
+                "[Vx HIP] FATAL: the topology %d is declared as two local "
+                "devices, %d and %d\n",
+                pair[0], local_devices[i].builtin, pair[1]);
+        abort();
+      }
+      return 1;
+    }
+    if (n == sizeof(local_devices) / sizeof(local_devices[0])) {
+      fprintf(stderr, "[Vx HIP] FATAL: more than %zu declared local devices\n",
+              n);
+      abort();
+    }
+    local_devices[n] = {pair[0], pair[1]};
+    local_device_count.store(n + 1, std::memory_order_release);
+    return 1;
+  }
+  case VX_HIP_CTRL_GEMM_KERNEL: {
+    /* payload -> int32_t: 0 automatic, 1 MFMA, 2 tiled. */
+    const int32_t *which = static_cast<const int32_t *>(payload);
+    if (!which || *which < 0 || *which > 2) {
+      return 0;
+    }
+    forced_gemm_kernel.store(*which);
+    return 1;
+  }
+  case VX_HIP_CTRL_STATS: {
+    /* payload -> int64_t[5]: routed GEMMs, of them MFMA, of them tiled, host
+     * fallbacks, bytes staged from host memory. */
+    int64_t *out = static_cast<int64_t *>(payload);
+    if (!out) {
+      return 0;
+    }
+    out[0] = stat_gemm_device.load();
+    out[1] = stat_gemm_mfma.load();
+    out[2] = stat_gemm_tiled.load();
+    out[3] = stat_host_fallback.load();
+    out[4] = stat_staged_bytes.load();
+    return 1;
+  }
+  case VX_HIP_CTRL_POOL_DRAIN:
+    if (hip_available()) {
+      wait_for_kernels("pool drain");
+      pool().drain();
+    }
+    return 1;
+  default:
+    return 0;
+  }
+}
+
+/* No TMA on AMD hardware: a kernel asking for a tensor map gets 0 and copies
+ * its tile itself (reference runtime/host_dispatch_common.h:727-738). */
+int64_t vx_plugin_tensor_map(int64_t base, int64_t rank, int64_t elem_bytes,
+                             int64_t d0, int64_t d1, int64_t d2, int64_t d3,
+                             int64_t d4, int64_t s0, int64_t s1, int64_t s2,
+                             int64_t s3, int64_t s4, int64_t b0, int64_t b1,
+                             int64_t b2, int64_t b3, int64_t b4) {
+  (void)base, (void)rank, (void)elem_bytes, (void)d0, (void)d1, (void)d2;
+  (void)d3, (void)d4, (void)s0, (void)s1, (void)s2, (void)s3, (void)s4;
+  (void)b0, (void)b1, (void)b2, (void)b3, (void)b4;
+  return 0;
+}
+
+/* The caller stream, as a hipStream_t. The CUDA-named pair is what compiled
+ * programs and host code already call (reference
+ * runtime/cuda_dispatch.cpp:2030-2035); the HIP-named pair is the same. */
+void vx_cuda_set_stream(void *stream) {
+  caller_stream = static_cast<hipStream_t>(stream);
+}
+void *vx_cuda_get_stream(void) { return caller_stream; }
+void vx_hip_set_stream(void *stream) {
+  caller_stream = static_cast<hipStream_t>(stream);
+}
+void *vx_hip_get_stream(void) { return caller_stream; }
+
+void vx_collective_init(int32_t rank, int32_t ranks) {
+  char msg[256];
+  if (one_rank_ranks) {
+    collective_fatal("vx_collective_init ran a second time. Call "
+                     "vx_collective_finish first.");
+  }
+  if (ranks != 1 || rank != 0) {
+    snprintf(msg, sizeof(msg),
+             "vx_collective_init got rank %d of %d ranks, but this process "
+             "runs a job of one rank only: this build joins no other GPUs.",
+             rank, ranks);
+    collective_fatal(msg);
+  }
+  one_rank_ranks = 1;
+}
+
+void vx_collective_finish(void) {
+  if (!one_rank_ranks) {
+    collective_fatal("vx_collective_finish ran before vx_collective_init.");
+  }
+  one_rank_ranks = 0;
+}
+
+int32_t vx_collective_rank(void) { return one_rank_ranks ? 0 : -1; }
+int32_t vx_collective_ranks(void) { return one_rank_ranks; }
+
+void vx_collective_all_reduce_sum_f32(const float *input, float *output,
+                                      int64_t count) {
+  one_rank_copy(input, output, count, 4, "vx_collective_all_reduce_sum_f32");
+}
+void vx_collective_all_reduce_sum_bf16(const uint16_t *input, uint16_t *output,
+                                       int64_t count) {
+  one_rank_copy(input, output, count, 2, "vx_collective_all_reduce_sum_bf16");
+}
+void vx_collective_all_gather_f32(const float *input, float *output,
+                                  int64_t count) {
+  one_rank_copy(input, output, count, 4, "vx_collective_all_gather_f32");
+}
+void vx_collective_all_gather_bf16(const uint16_t *input, uint16_t *output,
+                                   int64_t count) {
+  one_rank_copy(input, output, count, 2, "vx_collective_all_gather_bf16");
+}
+
+int64_t vx_host_worker_id(void) { return 0; }
+int64_t vx_host_worker_count(void) { return 1; }
+
+} // extern "C"

@@ -1,0 +1,31 @@
+/*
+ * vx_ops_kernels.h -- launchers of the library-op kernels (ops.cpp calls
+ * them after validating arguments). Each returns false for a shape or
+ * alignment its kernel does not take, and launches nothing then.
+ */
+#ifndef VX_AMD_OPS_KERNELS_H
+#define VX_AMD_OPS_KERNELS_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vxk {
+
+/* y[b, r] = scale[r] * sum_c w[r, c] * x[b, c]; cols % 16 == 0, batch 1..16,
+ * w and x 16-byte aligned. */
+bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
+                    float *y, int64_t rows, int64_t cols, int64_t batch,
+                    hipStream_t stream);
+
+/* Flash-attention forward; layout as include/vx_hip_ops.h. head_dim 64 or
+ * 128, seq lengths >= 1. */
+bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
+                           const uint16_t *v, uint16_t *o, float *lse,
+                           int64_t batch, int64_t heads, int64_t kv_heads,
+                           int64_t seq_q, int64_t seq_k, int64_t head_dim,
+                           float scale, bool causal, hipStream_t stream);
+
+} // namespace vxk
+
+#endif /* VX_AMD_OPS_KERNELS_H */

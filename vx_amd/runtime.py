@@ -1,0 +1,244 @@
+"""Host-side mirror of the Vx plugin ABI over libvx_hip_dispatch.so.
+
+This is what a compiled Vx program does at run time, spelled in Python so
+tests and the benchmark drive the library through the same C entry points:
+``transfer()`` is vx_plugin_alloc_and_transfer on Topology::GPU[0] (id 500),
+``c = a @ b`` is vx_plugin_dispatch_async with a kind=matmul payload, a host
+read is vx_plugin_transfer_device_to_host, and the vx_nn ops are the
+``extern "C"`` entry points of include/vx_hip_ops.h.
+
+The library is loaded from this package directory; nothing falls back to
+another implementation when it is missing.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+from . import abi
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libvx_hip_dispatch.so"
+
+_c_size = ctypes.c_size_t
+_vp = ctypes.c_void_p
+_i32, _i64, _u32, _u64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64
+
+# Every symbol include/vx_hardware_runtime.h and include/vx_hip_ops.h declare,
+# with (restype, argtypes).
+SIGNATURES = {
+    "vx_plugin_alloc_and_transfer": (_vp, [_c_size, _vp, _u32, _u32]),
+    "vx_plugin_alloc_and_transfer_async": (_vp, [_c_size, _vp, _u32, _u32]),
+    "vx_plugin_dispatch_async": (_u64, [_vp, _c_size, _vp, _vp, _i64]),
+    "vx_plugin_dispatch_async_flat": (_u64, [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int]),
+    "vx_plugin_await_future": (None, [_u64]),
+    "vx_plugin_transfer_device_to_host": (_i32, [_vp, _vp, _c_size, _u32]),
+    "vx_plugin_transfer_peer": (_vp, [_vp, _u32, _u32, _c_size]),
+    "vx_plugin_free": (None, [_vp, _u32]),
+    "vx_plugin_arrivals_take": (_vp, [_vp, _c_size, _vp, _u32, _u32]),
+    "vx_plugin_arrivals_give": (None, [_vp, _vp, _c_size, _u32]),
+    "vx_plugin_release_future": (None, [_u64]),
+    "vx_plugin_control": (_i32, [_u32, _vp]),
+    "vx_plugin_tensor_map": (_i64, [_i64] * 18),
+    "vx_cuda_set_stream": (None, [_vp]),
+    "vx_cuda_get_stream": (_vp, []),
+    "vx_collective_init": (None, [_i32, _i32]),
+    "vx_collective_finish": (None, []),
+    "vx_collective_rank": (_i32, []),
+    "vx_collective_ranks": (_i32, []),
+    "vx_collective_all_reduce_sum_f32": (None, [_vp, _vp, _i64]),
+    "vx_collective_all_reduce_sum_bf16": (None, [_vp, _vp, _i64]),
+    "vx_collective_all_gather_f32": (None, [_vp, _vp, _i64]),
+    "vx_collective_all_gather_bf16": (None, [_vp, _vp, _i64]),
+    "vx_host_worker_id": (_i64, []),
+    "vx_host_worker_count": (_i64, []),
+}
+
+HIP_SIGNATURES = {
+    "vx_hip_set_stream": (None, [_vp]),
+    "vx_hip_get_stream": (_vp, []),
+    "vx_nn_flash_attention_fwd_bf16": (
+        _i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i32]),
+    "vx_nn_gemv_i8_bf16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
+}
+
+
+def bind(lib: ctypes.CDLL, table: dict) -> None:
+    for name, (res, args) in table.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+class DispatchLibrary:
+    """A loaded dispatch library and the ABI calls on it."""
+
+    def __init__(self, path: os.PathLike | str = LIB_PATH, hip: bool = True):
+        path = Path(path)
+        if not path.exists():
+            raise FileNotFoundError(
+                f"{path} is not built; run `python -m vx_amd.build` (or __graft_entry__.build())")
+        self.path = path
+        self.lib = ctypes.CDLL(str(path), mode=ctypes.RTLD_GLOBAL)
+        bind(self.lib, SIGNATURES)
+        self.hip = hip
+        if hip:
+            bind(self.lib, HIP_SIGNATURES)
+
+    # -- lifecycle ---------------------------------------------------------
+    def device_count(self) -> int:
+        return self.lib.vx_plugin_control(abi.CTRL_GET_DEVICE_COUNT, None)
+
+    def control(self, opcode: int, payload=None) -> int:
+        return self.lib.vx_plugin_control(opcode, payload)
+
+    def wait(self, topo: int = abi.TOPO_GPU_BASE) -> None:
+        t = ctypes.c_int32(topo)
+        self.lib.vx_plugin_control(abi.CTRL_WAIT, ctypes.byref(t))
+
+    def stats(self) -> dict:
+        out = (ctypes.c_int64 * 5)()
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_STATS, out):
+            raise RuntimeError("the library answered no statistics")
+        return dict(gemm_device=out[0], gemm_mfma=out[1], gemm_tiled=out[2],
+                    host_fallback=out[3], staged_bytes=out[4])
+
+    def force_gemm_kernel(self, which: int) -> None:
+        v = ctypes.c_int32(which)
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMM_KERNEL, ctypes.byref(v)):
+            raise ValueError(f"no GEMM kernel {which}")
+
+    # -- memory ------------------------------------------------------------
+    def transfer(self, array: np.ndarray | None, nbytes: int | None = None,
+                 topo: int = abi.TOPO_GPU_BASE, space_access: int = 0) -> int:
+        """vx_plugin_alloc_and_transfer: a new allocation in `topo`'s memory
+        holding `array` (or `nbytes` uninitialised)."""
+        if array is not None:
+            array = np.ascontiguousarray(array)
+            nbytes = array.nbytes
+            src = array.ctypes.data
+        else:
+            src = None
+        ptr = self.lib.vx_plugin_alloc_and_transfer(nbytes, src, topo, space_access)
+        if not ptr:
+            raise MemoryError(f"vx_plugin_alloc_and_transfer({nbytes}) returned NULL")
+        return ptr
+
+    def fetch(self, ptr: int, out: np.ndarray, topo: int = abi.TOPO_GPU_BASE) -> np.ndarray:
+        assert out.flags.c_contiguous
+        self.lib.vx_plugin_transfer_device_to_host(ptr, out.ctypes.data, out.nbytes, topo)
+        return out
+
+    def free(self, ptr: int, topo: int = abi.TOPO_GPU_BASE) -> None:
+        self.lib.vx_plugin_free(ptr, topo)
+
+    # -- dispatch ------------------------------------------------------------
+    def dispatch(self, payload: bytes, args: abi.CallArgs) -> int:
+        buf = ctypes.create_string_buffer(payload, len(payload))
+        argv, tags, n = args.arrays()
+        return self.lib.vx_plugin_dispatch_async(buf, len(payload), argv, tags, n)
+
+
+class DeviceArray:
+    """An allocation from vx_plugin_alloc_and_transfer with its shape and
+    element type. `dtype` is an abi.DTYPE_* code; bf16/f16 travel as uint16."""
+
+    NP = {abi.DTYPE_F32: np.float32, abi.DTYPE_F64: np.float64, abi.DTYPE_BF16: np.uint16,
+          abi.DTYPE_F16: np.uint16, abi.DTYPE_I8: np.int8, abi.DTYPE_I32: np.int32,
+          abi.DTYPE_I64: np.int64}
+
+    def __init__(self, lib: DispatchLibrary, shape, dtype: int, host: np.ndarray | None = None,
+                 topo: int = abi.TOPO_GPU_BASE):
+        self.lib, self.shape, self.dtype, self.topo = lib, tuple(shape), dtype, topo
+        self.nbytes = int(np.prod(self.shape)) * abi.DTYPE_BYTES[dtype]
+        if host is not None:
+            host = np.ascontiguousarray(host, dtype=self.NP[dtype])
+            assert host.shape == self.shape, (host.shape, self.shape)
+        self.ptr = lib.transfer(host, self.nbytes, topo)
+
+    @classmethod
+    def of(cls, lib, host: np.ndarray, dtype: int, topo: int = abi.TOPO_GPU_BASE) -> "DeviceArray":
+        return cls(lib, host.shape, dtype, host, topo)
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.NP[self.dtype])
+        return self.lib.fetch(self.ptr, out, self.topo)
+
+    def descriptor(self, strides=None, offset: int = 0, sizes=None) -> abi.Descriptor:
+        return abi.Descriptor(self.ptr, sizes if sizes is not None else self.shape, strides, offset)
+
+    def free(self) -> None:
+        if self.ptr:
+            self.lib.free(self.ptr, self.topo)
+            self.ptr = 0
+
+
+def matmul(lib: DispatchLibrary, a: abi.Descriptor, a_dtype: int, b: abi.Descriptor,
+           b_dtype: int, out, out_dtype: int, outkind: str = "buffer",
+           topo: int = abi.TOPO_GPU_BASE) -> int:
+    """Dispatch ``out = a @ b`` in the argument shape the compiler emits for
+    `c = a @ b`: six launch operands, A at 0, B at 2, the result at 5, loop
+    bounds and the fill constant between (reference
+    tests/runtime/gemm_plan_test.cpp:130-175). `out` is a Descriptor (buffer
+    filled in place) or a SlotStorage (result published through the slot)."""
+    args = abi.CallArgs()
+    args.memref(a, a_dtype).scalar(0, abi.KIND_I64).memref(b, b_dtype)
+    args.scalar(1, abi.KIND_I64).scalar(0.0, abi.KIND_F32)
+    if isinstance(out, abi.SlotStorage):
+        args.slot(out, out_dtype, 2)
+    else:
+        args.memref(out, out_dtype)
+    return lib.dispatch(abi.matmul_payload(outkind=outkind, topo=topo), args)
+
+
+def flash_attention_fwd(lib: DispatchLibrary, q: int, k: int, v: int, o: int, lse: int | None,
+                        batch: int, heads: int, kv_heads: int, seq_q: int, seq_k: int,
+                        head_dim: int, scale: float, causal: bool) -> int:
+    return lib.lib.vx_nn_flash_attention_fwd_bf16(q, k, v, o, lse, batch, heads, kv_heads, seq_q,
+                                                  seq_k, head_dim, scale, 1 if causal else 0)
+
+
+def gemv_i8(lib: DispatchLibrary, w: int, scale: int, x: int, y: int, rows: int, cols: int,
+            batch: int) -> int:
+    return lib.lib.vx_nn_gemv_i8_bf16(w, scale, x, y, rows, cols, batch)
+
+
+class HipTimer:
+    """hipEvent timing on the stream the library launches on (the calling
+    thread's caller stream; the null stream by default)."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so", mode=ctypes.RTLD_GLOBAL)
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(_vp)]
+        self.hip.hipEventRecord.argtypes = [_vp, _vp]
+        self.hip.hipEventSynchronize.argtypes = [_vp]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), _vp, _vp]
+        self.hip.hipEventDestroy.argtypes = [_vp]
+        self.hip.hipDeviceSynchronize.argtypes = []
+
+    def event(self):
+        e = _vp()
+        self._check(self.hip.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e
+
+    def record(self, e, stream=None) -> None:
+        self._check(self.hip.hipEventRecord(e, stream), "hipEventRecord")
+
+    def elapsed_ms(self, start, stop) -> float:
+        self._check(self.hip.hipEventSynchronize(stop), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self._check(self.hip.hipEventElapsedTime(ctypes.byref(ms), start, stop),
+                    "hipEventElapsedTime")
+        return ms.value
+
+    def sync(self) -> None:
+        self._check(self.hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    @staticmethod
+    def _check(rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
