@@ -240,6 +240,24 @@ def test_mfma_and_tiled_agree(hiplib, rng):
     assert_max_abs(c1, c2, 1e-3, "mfma vs tiled")
 
 
+@pytest.mark.parametrize("out_dt", [abi.DTYPE_F32, abi.DTYPE_BF16])
+def test_mfma_variants_bit_identical(hiplib, out_dt, rng):
+    """Every MFMA kernel adds the same MFMA products in the same k order, so
+    their outputs are equal bit for bit (and match the oracle)."""
+    announce(f"gemm mfma variants out={out_dt}")
+    a16 = f32_to_bf16(rng.normal(0, 1, (512, 768)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1, (768, 1024)).astype(np.float32))
+    outs = []
+    for kern in (abi.GEMM_MFMA, abi.GEMM_MFMA_PIPE4, abi.GEMM_MFMA_PIPE8):
+        c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, out_dt, kernel=kern)
+        assert st["gemm_mfma"] == 1
+        outs.append(c)
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    got = outs[0] if out_dt == abi.DTYPE_F32 else bf16_to_f32(outs[0])
+    assert_max_abs(got, oracle.gemm_bf16_f32(a16, b16), 0.2 if out_dt == abi.DTYPE_BF16 else 1e-3,
+                   "variants vs oracle")
+
+
 def test_flat_matvec(hiplib, rng):
     """vx_plugin_dispatch_async_flat: xout[i] = sum_j w[i*n+j] x[j]."""
     announce("flat matvec")

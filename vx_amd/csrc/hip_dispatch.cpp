@@ -262,7 +262,9 @@ bool run_gemm(const vx_gemm_plan &plan) {
 
   vxk::GemmKernel which = vxk::gemm_pick(g);
   const int forced = forced_gemm_kernel.load();
-  if (forced == vxk::GEMM_MFMA_256 || forced == vxk::GEMM_TILED) {
+  if (forced != 0 && (forced == vxk::GEMM_TILED || vxk::gemm_is_mfma(which))) {
+    /* A forced MFMA variant applies only where an MFMA kernel takes the
+     * shape; the tiled kernel takes every shape. */
     which = (vxk::GemmKernel)forced;
   }
 
@@ -293,7 +295,7 @@ bool run_gemm(const vx_gemm_plan &plan) {
     (void)hipEventDestroy(t1);
   }
   ++stat_gemm_device;
-  (which == vxk::GEMM_MFMA_256 ? stat_gemm_mfma : stat_gemm_tiled)++;
+  (vxk::gemm_is_mfma(which) ? stat_gemm_mfma : stat_gemm_tiled)++;
   started_kernel("a GEMM");
 
   if (out_is_device) {
@@ -722,9 +724,10 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     return 1;
   }
   case VX_HIP_CTRL_GEMM_KERNEL: {
-    /* payload -> int32_t: 0 automatic, 1 MFMA, 2 tiled. */
+    /* payload -> int32_t: 0 automatic, 1 MFMA (plain), 2 tiled, 3 MFMA
+     * pipelined on 4 waves, 4 MFMA pipelined on 8 waves. */
     const int32_t *which = static_cast<const int32_t *>(payload);
-    if (!which || *which < 0 || *which > 2) {
+    if (!which || *which < 0 || *which > 4) {
       return 0;
     }
     forced_gemm_kernel.store(*which);

@@ -28,6 +28,8 @@
 #include "../vx_hip_common.h"
 #include "../vx_kernels.h"
 
+#include <type_traits>
+
 namespace vxk {
 namespace {
 
@@ -35,6 +37,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileM = 256;
 constexpr int kTileN = 256;
@@ -227,6 +230,180 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_256(
   }
 }
 
+/* Software-pipelined variant of the same 256x256x64 tile, for kWavesM x
+ * kWavesN waves (4 = one wave per SIMD, 8 = two).
+ *
+ * Per stage (K step of 64) the wave walks 4 k-substeps of 16. The MFMA
+ * operands of substep s+1 are read from LDS into a second register set
+ * before the MFMAs of substep s issue (sched_barrier keeps that order), so
+ * LDS latency hides behind MFMA work instead of stalling it. The global
+ * loads of the stage after next are issued after substep 2 and land in
+ * registers; they are written into the idle LDS buffer after substep 1 of
+ * the following stage, leaving a whole stage for the loads to arrive. One
+ * barrier per stage. B's 8-row blocks are kNB columns wide (8 for 256
+ * threads, 4 for 512) so each thread owns exactly one block. */
+template <int kWavesM, int kWavesN, bool kBf16, int kOut>
+__global__ __launch_bounds__(64 * kWavesM * kWavesN, 1) void gemm_mfma_pipe(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
+    int tiles_m, int tiles_n) {
+  constexpr int kT = 64 * kWavesM * kWavesN;
+  constexpr int kTM = kTileM / kWavesM / 32; /* 32x32 tiles per wave in m */
+  constexpr int kTN = kTileN / kWavesN / 32;
+  constexpr int kALoads = kTileM * kChunks / kT;
+  constexpr int kNB = kTileN * kChunks / kT; /* B block width: 8 or 4 */
+  static_assert(kNB == 8 || kNB == 4, "one B block per thread");
+  __shared__ u32x4 lds[2][2][kTileM * kChunks];
+
+  const int t = threadIdx.x;
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) {
+    id = (id & 7) * (nwg >> 3) + (id >> 3);
+  }
+  const int group_size = kGroupM * tiles_n;
+  const int first_m = (id / group_size) * kGroupM;
+  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int in_group = id % group_size;
+  const int tm = first_m + in_group % rows_in_group;
+  const int tn = in_group / rows_in_group;
+  const int64_t m0 = (int64_t)tm * kTileM;
+  const int64_t n0 = (int64_t)tn * kTileN;
+
+  const uint16_t *a_src = A + (m0 + (t >> 3)) * lda + (t & 7) * 8;
+  const int64_t a_pass = (int64_t)(kT / 8) * lda;
+  const int kc = t & 7;
+  const int nb = t >> 3;
+  const uint16_t *b_src = B + (int64_t)(kc * 8) * ldb + n0 + nb * kNB;
+
+  using BRow = typename std::conditional<kNB == 8, u32x4, u32x2>::type;
+  u32x4 areg[kALoads];
+  BRow breg[8]; /* one row of the thread's 8 x kNB block of B */
+
+  auto fetch = [&](int step) {
+    const uint16_t *ap = a_src + (int64_t)step * kStageK;
+#pragma unroll
+    for (int p = 0; p < kALoads; ++p) {
+      areg[p] = *reinterpret_cast<const u32x4 *>(ap + p * a_pass);
+    }
+    const uint16_t *bp = b_src + (int64_t)step * kStageK * ldb;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      breg[r] = *reinterpret_cast<const BRow *>(bp + r * ldb);
+    }
+  };
+
+  auto stash = [&](int s) {
+    u32x4 *la = lds[s][0];
+#pragma unroll
+    for (int p = 0; p < kALoads; ++p) {
+      const int row = p * (kT / 8) + (t >> 3);
+      la[row * kChunks + swz(row, t & 7)] = areg[p];
+    }
+    u32x4 *lb = lds[s][1];
+#pragma unroll
+    for (int w = 0; w < kNB / 2; ++w) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t x = breg[2 * q][w];
+        const uint32_t y = breg[2 * q + 1][w];
+        lo[q] = (x & 0xffffu) | (y << 16);
+        hi[q] = (x >> 16) | (y & 0xffff0000u);
+      }
+      const int row = nb * kNB + 2 * w;
+      lb[row * kChunks + swz(row, kc)] = lo;
+      lb[(row + 1) * kChunks + swz(row + 1, kc)] = hi;
+    }
+  };
+
+  f32x16 acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+      }
+    }
+  }
+
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int wm = wave / kWavesN;
+  const int wn = wave % kWavesN;
+  const int lrow = lane & 31;
+  const int lk = lane >> 5;
+  const int a_row0 = wm * (kTileM / kWavesM) + lrow;
+  const int b_row0 = wn * (kTileN / kWavesN) + lrow;
+
+  u32x4 fa[2][kTM], fb[2][kTN];
+  auto frags = [&](int s, int ks, u32x4 *af, u32x4 *bfr) {
+    const u32x4 *la = lds[s][0];
+    const u32x4 *lb = lds[s][1];
+    const int c = ks * 2 + lk;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const int row = a_row0 + i * 32;
+      af[i] = la[row * kChunks + swz(row, c)];
+    }
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int row = b_row0 + j * 32;
+      bfr[j] = lb[row * kChunks + swz(row, c)];
+    }
+  };
+
+  const int steps = K / kStageK;
+  fetch(0);
+  stash(0);
+  if (steps > 1) {
+    fetch(1);
+  }
+  __syncthreads();
+  for (int step = 0; step < steps; ++step) {
+    const int s = step & 1;
+    frags(s, 0, fa[0], fb[0]);
+#pragma unroll
+    for (int ks = 0; ks < kStageK / 16; ++ks) {
+      if (ks + 1 < kStageK / 16) {
+        frags(s, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+        for (int j = 0; j < kTN; ++j) {
+          acc[i][j] = mfma32<kBf16>(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks == 1 && step + 1 < steps) {
+        stash(s ^ 1);
+      }
+      if (ks == 2 && step + 2 < steps) {
+        fetch(step + 2);
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int64_t col = n0 + wn * (kTileN / kWavesN) + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * (kTileM / kWavesM) + i * 32 + 8 * (r >> 2) +
+                            4 * lk + (r & 3);
+        put<kOut>(C, row * ldc + col, acc[i][j][r]);
+      }
+    }
+  }
+}
+
 template <int kIn>
 __device__ __forceinline__ auto load_in(const void *p, int64_t at) {
   if constexpr (kIn == VX_DTYPE_F64) {
@@ -361,6 +538,29 @@ void launch_mfma(const GemmArgs &g, hipStream_t s) {
                      g.ldb, g.ldc, tiles_m, tiles_n);
 }
 
+template <int kWM, int kWN, bool kBf16, int kOut>
+void launch_pipe(const GemmArgs &g, hipStream_t s) {
+  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
+  hipLaunchKernelGGL((gemm_mfma_pipe<kWM, kWN, kBf16, kOut>),
+                     dim3(tiles_m * tiles_n), dim3(64 * kWM * kWN), 0, s,
+                     static_cast<const uint16_t *>(g.a),
+                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
+                     g.ldb, g.ldc, tiles_m, tiles_n);
+}
+
+template <int kWM, int kWN>
+void launch_pipe_any(const GemmArgs &g, hipStream_t s) {
+  const bool bf = g.in_dtype == VX_DTYPE_BF16;
+  if (g.out_dtype == VX_DTYPE_F32) {
+    bf ? launch_pipe<kWM, kWN, true, VX_DTYPE_F32>(g, s)
+       : launch_pipe<kWM, kWN, false, VX_DTYPE_F32>(g, s);
+  } else if (bf) {
+    launch_pipe<kWM, kWN, true, VX_DTYPE_BF16>(g, s);
+  } else {
+    launch_pipe<kWM, kWN, false, VX_DTYPE_F16>(g, s);
+  }
+}
+
 template <int kIn, int kOut>
 void launch_tiled(const GemmArgs &g, hipStream_t s) {
   dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((g.m + 63) / 64));
@@ -372,7 +572,7 @@ void launch_tiled(const GemmArgs &g, hipStream_t s) {
 
 GemmKernel gemm_pick(const GemmArgs &g) {
   if (mfma_takes(g)) {
-    return GEMM_MFMA_256;
+    return GEMM_MFMA_PIPE4;
   }
   if (tiled_takes(g)) {
     return GEMM_TILED;
@@ -395,6 +595,12 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
     } else {
       launch_mfma<false, VX_DTYPE_F16>(g, stream);
     }
+  } else if (which == GEMM_MFMA_PIPE4 || which == GEMM_MFMA_PIPE8) {
+    if (!mfma_takes(g)) {
+      return false;
+    }
+    which == GEMM_MFMA_PIPE4 ? launch_pipe_any<2, 2>(g, stream)
+                             : launch_pipe_any<2, 4>(g, stream);
   } else if (which == GEMM_TILED) {
     if (!tiled_takes(g)) {
       return false;

@@ -32,7 +32,13 @@ enum GemmKernel {
   GEMM_NONE = 0,
   GEMM_MFMA_256 = 1, /* bf16/f16 MFMA 32x32x16, 256x256x64 tiles */
   GEMM_TILED = 2,    /* any supported type, 64x64 tiles, exact k order */
+  GEMM_MFMA_PIPE4 = 3, /* as 1, software-pipelined, 4 waves */
+  GEMM_MFMA_PIPE8 = 4, /* as 1, software-pipelined, 8 waves */
 };
+
+inline bool gemm_is_mfma(GemmKernel k) {
+  return k == GEMM_MFMA_256 || k == GEMM_MFMA_PIPE4 || k == GEMM_MFMA_PIPE8;
+}
 
 GemmKernel gemm_pick(const GemmArgs &g);
 /* Launch; false when no kernel takes the arguments. */
