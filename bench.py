@@ -191,6 +191,24 @@ def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
                        f"{dt:.1f} s), oracle/vx_oracle.c loop nest, 1 thread")
 
 
+def copy_probe() -> int:
+    """A plain copy of known size: 256 MiB read and 256 MiB written per
+    launch, three launches."""
+    from vx_amd.runtime import DispatchLibrary, HipTimer
+
+    lib = DispatchLibrary()
+    timer = HipTimer()
+    nbytes = 256 * 2**20
+    src = lib.transfer(np.ones(nbytes // 4, np.float32))
+    for _ in range(3):
+        dst = lib.lib.vx_plugin_transfer_peer(src, 500, 500, nbytes)
+        timer.sync()
+        lib.free(dst)
+    lib.free(src)
+    log(f"copied {nbytes} bytes device to device 3 times")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,7 +216,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", default="gemm,fa,gemv,decode")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 256 MiB device to device through vx_plugin_transfer_peer, "
+                         "three times: the reference launch for scaling rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE readings to bytes")
     ns = ap.parse_args()
+    if ns.copy_probe:
+        return copy_probe()
     if ns.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (its sharding is a "
               "design in DESIGN.md). Run with --gpus 1.", file=sys.stderr)

@@ -63,6 +63,72 @@ int32_t vx_nn_gemv_i8_bf16(const int8_t *w, const float *scale,
                            const uint16_t *x, float *y, int64_t rows,
                            int64_t cols, int64_t batch);
 
+/* Greedy int8 decode of a Llama-2-style model, resident in HBM.
+ *
+ * The token step of reference examples/llama.vx:173-420 (RMSNorm eps 1e-5,
+ * Q/K/V, RoPE, KV cache, causal attention, Wo, SwiGLU FFN, residuals, final
+ * RMSNorm, classifier sharing the embedding table, argmax with the lowest
+ * index winning a tie) as GPU library ops: every linear is an int8
+ * weight-only GEMV with per-row f32 scales whose input is rounded to bf16;
+ * everything else is f32. The position and the next token stay on the GPU,
+ * so a whole step is replayable as one hipGraph with no host round trip.
+ *
+ * Weights are host pointers in llama2.c order, matrices [out][in]:
+ * tok [vocab, dim] (embedding and classifier); per layer wq [dim, dim],
+ * wk/wv [kv_dim, dim], wo [dim, dim], w1/w3 [hidden, dim], w2 [dim, hidden],
+ * each with one f32 scale per row; RMSNorm weights f32; `rope` the
+ * [seq_len, head_size / 2] table of (cos, sin) of the rotary angles. */
+typedef struct vx_llama_i8_config {
+  int32_t dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len;
+} vx_llama_i8_config;
+
+typedef struct vx_llama_i8_weights {
+  const int8_t *tok_q;
+  const float *tok_s;
+  const float *rms_att; /* [layers, dim] */
+  const int8_t *wq_q;
+  const float *wq_s;
+  const int8_t *wk_q;
+  const float *wk_s;
+  const int8_t *wv_q;
+  const float *wv_s;
+  const int8_t *wo_q;
+  const float *wo_s;
+  const float *rms_ffn; /* [layers, dim] */
+  const int8_t *w1_q;
+  const float *w1_s;
+  const int8_t *w2_q;
+  const float *w2_s;
+  const int8_t *w3_q;
+  const float *w3_s;
+  const float *rms_final; /* [dim] */
+  const float *rope;      /* [seq_len, head_size / 2, 2] */
+} vx_llama_i8_weights;
+
+/* Capture one token step as a hipGraph and replay it (else: stream
+ * launches, one by one). */
+#define VX_LLAMA_GRAPH 1
+
+/* Upload a model to GPU[topology_id - 500]; NULL (and a [Vx HIP] line) when
+ * the config is not one the kernels take or there is no GPU. */
+void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
+                         const vx_llama_i8_weights *w, uint32_t topology_id);
+
+/* Feed prompt[0..n_prompt), then generate n_steps tokens greedily into
+ * out_tokens; out_margin (may be NULL) gets each generated token's logit
+ * lead over the runner-up. Returns 0, or a VX_OP_E* code. */
+int32_t vx_llama_i8_generate(void *model, const int32_t *prompt,
+                             int32_t n_prompt, int32_t n_steps,
+                             int32_t *out_tokens, float *out_margin,
+                             int32_t flags);
+
+/* Feed tokens[0..n) at positions 0..n-1 and copy the logits after each
+ * position to logits[n, vocab]. Returns 0 or a VX_OP_E* code. */
+int32_t vx_llama_i8_logits(void *model, const int32_t *tokens, int32_t n,
+                           float *logits);
+
+void vx_llama_i8_destroy(void *model);
+
 #ifdef __cplusplus
 }
 #endif

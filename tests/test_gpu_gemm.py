@@ -253,9 +253,15 @@ def test_mfma_variants_bit_identical(hiplib, out_dt, rng):
         assert st["gemm_mfma"] == 1
         outs.append(c)
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
-    got = outs[0] if out_dt == abi.DTYPE_F32 else bf16_to_f32(outs[0])
-    assert_max_abs(got, oracle.gemm_bf16_f32(a16, b16), 0.2 if out_dt == abi.DTYPE_BF16 else 1e-3,
-                   "variants vs oracle")
+    want = oracle.gemm_bf16_f32(a16, b16)
+    if out_dt == abi.DTYPE_F32:
+        assert_max_abs(outs[0], want, 1e-3, "variants vs oracle")
+    else:
+        # one rounding of an f32 value that differs from the oracle's only in
+        # summation order (by < 1e-3 here, as the f32 case shows): within one
+        # bf16 ulp (at most 2^-7 relative) plus that difference
+        got = bf16_to_f32(outs[0])
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-3)
 
 
 def test_flat_matvec(hiplib, rng):
