@@ -1,0 +1,103 @@
+"""The GPU int8 decode path against the CPU oracle: logits position by
+position on a small model, identical greedy token streams on the small
+model and on BASELINE config 4 (against the committed oracle fixture)."""
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import announce
+from vx_amd.decode import LlamaI8
+from vx_amd.llama import CONFIG_DECODE, CONFIG_TINY, LlamaConfig, make_model, make_prompt
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "decode_config4.json"
+
+
+def assert_same_tokens(got, want, margin):
+    """Identical greedy streams; a disagreement is reported with the logit
+    margin the oracle had at that step."""
+    got, want = list(map(int, got)), list(map(int, want))
+    if got != want:
+        i = next(k for k in range(len(want)) if got[k] != want[k])
+        raise AssertionError(f"token {i}: gpu {got[i]} vs oracle {want[i]} "
+                             f"(oracle margin there {margin[i]:.3g})")
+
+
+@pytest.mark.parametrize("cfg", [CONFIG_TINY,
+                                 LlamaConfig(dim=128, hidden_dim=256, n_layers=3, n_heads=2,
+                                             n_kv_heads=1, vocab_size=512, seq_len=96)])
+def test_logits_per_position_match_oracle(hiplib, cfg):
+    announce(f"decode logits {cfg}")
+    weights = make_model(cfg, seed=3)
+    tokens = list(make_prompt(cfg, n=20, seed=5))
+    model = LlamaI8(hiplib, cfg, weights)
+    got = model.logits(tokens)
+    model.close()
+    kv = np.zeros(2 * cfg.n_layers * cfg.seq_len * cfg.kv_dim, np.float32)
+    for pos, tok in enumerate(tokens):
+        want = oracle.llama_forward(cfg.as_dict(), weights, kv, int(tok), pos)
+        scale = float(np.abs(want).max())
+        err = float(np.abs(got[pos] - want).max())
+        assert err <= 1e-3 * scale + 1e-5, f"position {pos}: max abs error {err} (scale {scale})"
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_tiny_greedy_stream_matches_oracle(hiplib, graph):
+    announce(f"decode tiny greedy graph={graph}")
+    cfg = CONFIG_TINY
+    weights = make_model(cfg, seed=3)
+    prompt = make_prompt(cfg, n=6, seed=5)
+    want, margin = oracle.llama_generate(cfg.as_dict(), weights, prompt, 40)
+    model = LlamaI8(hiplib, cfg, weights)
+    got, gm = model.generate(prompt, 40, graph=graph)
+    model.close()
+    assert_same_tokens(got, want, margin)
+    np.testing.assert_allclose(gm, margin, atol=1e-3)
+
+
+def test_config4_greedy_stream_matches_oracle(hiplib):
+    """BASELINE config 4, 16-token prompt, 256 greedy tokens: the same stream
+    as the CPU oracle (tests/golden/make_decode_golden.py)."""
+    announce("decode config 4 greedy 256")
+    g = json.loads(GOLDEN.read_text())
+    cfg = CONFIG_DECODE
+    assert g["config"] == cfg.as_dict()
+    weights = make_model(cfg, seed=g["model_seed"])
+    prompt = make_prompt(cfg, n=16, seed=g["prompt_seed"])
+    assert list(map(int, prompt)) == g["prompt"]
+    model = LlamaI8(hiplib, cfg, weights)
+    got, gm = model.generate(prompt, g["n_steps"])
+    again, _ = model.generate(prompt, g["n_steps"])
+    model.close()
+    assert np.array_equal(got, again), "two runs of the same generation differ"
+    assert_same_tokens(got, g["tokens"], g["margins"])
+    np.testing.assert_allclose(gm, g["margins"], atol=2e-4)
+    # logits at the probed positions of the same sequence
+    model = LlamaI8(hiplib, cfg, weights)
+    seq = g["prompt"] + g["tokens"][:-1]
+    logits = model.logits(seq)
+    model.close()
+    for pos, probe in g["logit_probes"].items():
+        row = logits[int(pos)]
+        assert list(np.argsort(-row, kind="stable")[:4]) == probe["index"][:4], f"position {pos}"
+        np.testing.assert_allclose(row[probe["index"]], probe["value"], atol=2e-4,
+                                   err_msg=f"position {pos}")
+
+
+def test_refusals(hiplib):
+    announce("decode refusals")
+    cfg = LlamaConfig(dim=96, hidden_dim=128, n_layers=1, n_heads=5, n_kv_heads=5,
+                      vocab_size=64, seq_len=16)  # dim not a multiple of n_heads
+    with pytest.raises(RuntimeError):
+        LlamaI8(hiplib, cfg, make_model(CONFIG_TINY, seed=0))
+    model = LlamaI8(hiplib, CONFIG_TINY, make_model(CONFIG_TINY, seed=0))
+    with pytest.raises(RuntimeError):
+        model.generate([1, 2, 3], CONFIG_TINY.seq_len)  # past seq_len
+    with pytest.raises(RuntimeError):
+        model.generate([CONFIG_TINY.vocab_size], 4)  # token outside the vocabulary
+    model.close()

@@ -290,6 +290,24 @@ def test_oracle_llama_generate_greedy_is_argmax_chain():
     assert np.all(margin >= 0)
 
 
+def test_decode_golden_fixture_prefix():
+    """The committed config-4 fixture is the oracle's: its first tokens are
+    recomputed here (the whole stream takes the oracle ~85 s)."""
+    import json
+    from pathlib import Path
+    from vx_amd.llama import CONFIG_DECODE
+
+    g = json.loads((Path(__file__).parent / "golden" / "decode_config4.json").read_text())
+    cfg = CONFIG_DECODE
+    assert g["config"] == cfg.as_dict()
+    model = make_model(cfg, seed=g["model_seed"])
+    prompt = make_prompt(cfg, n=16, seed=g["prompt_seed"])
+    assert list(map(int, prompt)) == g["prompt"]
+    toks, margin = oracle.llama_generate(cfg.as_dict(), model, prompt, 3)
+    assert list(map(int, toks)) == g["tokens"][:3]
+    np.testing.assert_allclose(margin, g["margins"][:3], rtol=1e-6)
+
+
 def test_checker_catches_planted_error(rng):
     """The comparison the GPU tests use fails when one value of the oracle's
     answer is moved by more than the tolerance (the conformance harness's

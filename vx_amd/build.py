@@ -55,7 +55,7 @@ def sources() -> list[Path]:
 
 
 def _compile(src: Path, verbose: bool) -> Path:
-    obj = BUILD / (src.stem + ".o")
+    obj = BUILD / f"{src.parent.name}_{src.stem}.o"
     cmd = [hipcc(), *HIP_FLAGS, f"-I{FFI_INC}", "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]

@@ -1,0 +1,374 @@
+/*
+ * decode.cpp -- vx_llama_i8_*: an int8 Llama-2-style decoder resident in HBM
+ * and its greedy generation loop (include/vx_hip_ops.h).
+ *
+ * Weights are re-laid out once at upload so each fused kernel streams one
+ * matrix: per layer [Wq; Wk; Wv] stacked (one GEMV feeds RoPE and the KV
+ * cache) and W1/W3 interleaved row by row (one GEMV feeds SwiGLU). The
+ * position and the next token live in device memory; a step is a fixed
+ * sequence of 5 * layers + 2 launches that, with VX_LLAMA_GRAPH, is captured
+ * once into a hipGraph and replayed per token with no host synchronisation
+ * until the tokens are read back.
+ */
+#include "../../include/vx_hardware_runtime.h"
+#include "../../include/vx_hip_ops.h"
+#include "vx_decode_kernels.h"
+#include "vx_hip_common.h"
+#include "vx_ops_internal.h"
+
+#include <cstring>
+#include <vector>
+
+namespace {
+
+struct LlamaI8 {
+  vx_llama_i8_config cfg;
+  int hs = 0, kv_dim = 0, device = 0;
+  int8_t *tok_q = nullptr, *wqkv = nullptr, *wo = nullptr, *w13 = nullptr,
+         *w2 = nullptr;
+  float *tok_s = nullptr, *sqkv = nullptr, *so = nullptr, *s13 = nullptr,
+        *s2 = nullptr;
+  float *rms_att = nullptr, *rms_ffn = nullptr, *rms_final = nullptr,
+        *rope = nullptr;
+  float *kcache = nullptr, *vcache = nullptr;
+  float *x = nullptr, *q = nullptr, *logits = nullptr;
+  uint16_t *att16 = nullptr, *hb16 = nullptr;
+  int *pos = nullptr, *prompt = nullptr, *out_tokens = nullptr;
+  float *out_margin = nullptr;
+  int prompt_cap = 0, out_cap = 0;
+  hipStream_t stream = nullptr;
+  std::vector<void *> owned;
+};
+
+template <typename T> T *upload(LlamaI8 &m, const T *host, size_t count) {
+  void *p = nullptr;
+  VX_HIP_CHECK(hipMalloc(&p, count * sizeof(T) + 16));
+  if (host) {
+    VX_HIP_CHECK(hipMemcpy(p, host, count * sizeof(T), hipMemcpyHostToDevice));
+  }
+  m.owned.push_back(p);
+  return static_cast<T *>(p);
+}
+
+template <typename T> T *alloc(LlamaI8 &m, size_t count) {
+  return upload<T>(m, nullptr, count);
+}
+
+void release(LlamaI8 &m) {
+  if (m.stream) {
+    (void)hipStreamSynchronize(m.stream);
+    (void)hipStreamDestroy(m.stream);
+  }
+  for (void *p : m.owned) {
+    (void)hipFree(p);
+  }
+  m.owned.clear();
+}
+
+int32_t refuse(int32_t code, const char *why) {
+  fprintf(stderr, "[Vx HIP] vx_llama_i8: %s\n", why);
+  return code;
+}
+
+bool ensure_io(LlamaI8 &m, int n_prompt, int n_out) {
+  if (n_prompt > m.prompt_cap) {
+    m.prompt = alloc<int>(m, (size_t)n_prompt);
+    m.prompt_cap = n_prompt;
+  }
+  if (n_out > m.out_cap) {
+    m.out_tokens = alloc<int>(m, (size_t)n_out);
+    m.out_margin = alloc<float>(m, (size_t)n_out);
+    m.out_cap = n_out;
+  }
+  return true;
+}
+
+vxk::StepArgmaxArgs argmax_args(LlamaI8 &m, int n_prompt) {
+  vxk::StepArgmaxArgs a;
+  a.logits = m.logits;
+  a.vocab = m.cfg.vocab_size;
+  a.pos = m.pos;
+  a.prompt = m.prompt;
+  a.n_prompt = n_prompt;
+  a.out_tokens = m.out_tokens;
+  a.out_margin = m.out_margin;
+  a.out_cap = m.out_cap;
+  a.tok_q = m.tok_q;
+  a.tok_s = m.tok_s;
+  a.x = m.x;
+  a.dim = m.cfg.dim;
+  return a;
+}
+
+/* One token step on the model's stream. */
+void enqueue_step(LlamaI8 &m, int n_prompt) {
+  const vx_llama_i8_config &c = m.cfg;
+  const int qkv_rows = c.dim + 2 * m.kv_dim;
+  const int64_t layer_kv = (int64_t)c.seq_len * m.kv_dim;
+  for (int l = 0; l < c.n_layers; ++l) {
+    vxk::StepGemvArgs g{};
+    g.pos = m.pos;
+    g.dim = c.dim;
+    g.kv_dim = m.kv_dim;
+    g.hs = m.hs;
+    g.rope = m.rope;
+    g.kcache = m.kcache + l * layer_kv;
+    g.vcache = m.vcache + l * layer_kv;
+
+    vxk::StepGemvArgs qkv = g;
+    qkv.w = m.wqkv + (int64_t)l * qkv_rows * c.dim;
+    qkv.scale = m.sqkv + (int64_t)l * qkv_rows;
+    qkv.rows = qkv_rows;
+    qkv.cols = c.dim;
+    qkv.x = m.x;
+    qkv.norm = m.rms_att + (int64_t)l * c.dim;
+    qkv.out = m.q;
+    vxk::step_gemv_qkv(qkv, m.stream);
+
+    vxk::StepAttnArgs at;
+    at.q = m.q;
+    at.kcache = g.kcache;
+    at.vcache = g.vcache;
+    at.att16 = m.att16;
+    at.pos = m.pos;
+    at.kv_dim = m.kv_dim;
+    at.hs = m.hs;
+    at.kv_mul = c.n_heads / c.n_kv_heads;
+    vxk::step_attention_launch(at, c.n_heads, c.seq_len, m.stream);
+
+    vxk::StepGemvArgs wo = g;
+    wo.w = m.wo + (int64_t)l * c.dim * c.dim;
+    wo.scale = m.so + (int64_t)l * c.dim;
+    wo.rows = c.dim;
+    wo.cols = c.dim;
+    wo.in16 = m.att16;
+    wo.out = m.x;
+    vxk::step_gemv_resid(wo, m.stream);
+
+    vxk::StepGemvArgs ffn = g;
+    ffn.w = m.w13 + (int64_t)l * 2 * c.hidden_dim * c.dim;
+    ffn.scale = m.s13 + (int64_t)l * 2 * c.hidden_dim;
+    ffn.rows = 2 * c.hidden_dim;
+    ffn.cols = c.dim;
+    ffn.x = m.x;
+    ffn.norm = m.rms_ffn + (int64_t)l * c.dim;
+    ffn.out16 = m.hb16;
+    vxk::step_gemv_swiglu(ffn, m.stream);
+
+    vxk::StepGemvArgs w2 = g;
+    w2.w = m.w2 + (int64_t)l * c.dim * c.hidden_dim;
+    w2.scale = m.s2 + (int64_t)l * c.dim;
+    w2.rows = c.dim;
+    w2.cols = c.hidden_dim;
+    w2.in16 = m.hb16;
+    w2.out = m.x;
+    vxk::step_gemv_resid(w2, m.stream);
+  }
+  vxk::StepGemvArgs lg{};
+  lg.w = m.tok_q;
+  lg.scale = m.tok_s;
+  lg.rows = c.vocab_size;
+  lg.cols = c.dim;
+  lg.x = m.x;
+  lg.norm = m.rms_final;
+  lg.out = m.logits;
+  lg.pos = m.pos;
+  vxk::step_gemv_logits(lg, m.stream);
+  vxk::step_argmax_launch(argmax_args(m, n_prompt), m.stream);
+}
+
+} // namespace
+
+extern "C" {
+
+void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
+                         const vx_llama_i8_weights *w, uint32_t topology_id) {
+  if (!vxops::device_present()) {
+    refuse(VX_OP_ENODEV, "no GPU; this op has no host copy");
+    return nullptr;
+  }
+  if (!cfg || !w) {
+    refuse(VX_OP_EINVAL, "config and weights must not be NULL");
+    return nullptr;
+  }
+  const vx_llama_i8_config c = *cfg;
+  if (c.dim <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.n_layers <= 0 ||
+      c.hidden_dim <= 0 || c.vocab_size <= 0 || c.seq_len <= 0 ||
+      c.dim % c.n_heads || c.n_heads % c.n_kv_heads) {
+    refuse(VX_OP_EINVAL, "config extents must be positive, dim a multiple "
+                         "of n_heads and n_heads of n_kv_heads");
+    return nullptr;
+  }
+  const int hs = c.dim / c.n_heads;
+  const int kv_dim = c.dim * c.n_kv_heads / c.n_heads;
+  if (hs % 2 || hs > 256 || 256 % hs || !vxk::step_gemv_ok(c.dim, c.dim) ||
+      !vxk::step_gemv_ok(2 * c.hidden_dim, c.dim) ||
+      !vxk::step_gemv_ok(c.dim, c.hidden_dim) ||
+      !vxk::step_gemv_ok(c.vocab_size, c.dim) || kv_dim % 2 ||
+      c.seq_len > 16384) {
+    refuse(VX_OP_EUNSUPP, "shape not taken by the decode kernels (head size "
+                          "must divide 256; dim and hidden_dim multiples of "
+                          "16 and at most 4096; vocab even; seq_len <= 16384)");
+    return nullptr;
+  }
+  const int device =
+      vx_topology_device_index((int32_t)topology_id, VX_TOPO_GPU_BASE);
+  if (device < 0) {
+    refuse(VX_OP_EINVAL, "topology_id must name a GPU (500 + index)");
+    return nullptr;
+  }
+  VX_HIP_CHECK(hipSetDevice(device));
+
+  LlamaI8 *m = new LlamaI8();
+  m->cfg = c;
+  m->hs = hs;
+  m->kv_dim = kv_dim;
+  m->device = device;
+  const size_t L = (size_t)c.n_layers, D = (size_t)c.dim,
+               H = (size_t)c.hidden_dim, KV = (size_t)kv_dim;
+  const size_t qkv_rows = D + 2 * KV;
+
+  /* [Wq; Wk; Wv] per layer, with their scales. */
+  std::vector<int8_t> qkv(L * qkv_rows * D);
+  std::vector<float> sqkv(L * qkv_rows);
+  for (size_t l = 0; l < L; ++l) {
+    int8_t *dst = qkv.data() + l * qkv_rows * D;
+    memcpy(dst, w->wq_q + l * D * D, D * D);
+    memcpy(dst + D * D, w->wk_q + l * KV * D, KV * D);
+    memcpy(dst + (D + KV) * D, w->wv_q + l * KV * D, KV * D);
+    float *sd = sqkv.data() + l * qkv_rows;
+    memcpy(sd, w->wq_s + l * D, D * 4);
+    memcpy(sd + D, w->wk_s + l * KV, KV * 4);
+    memcpy(sd + D + KV, w->wv_s + l * KV, KV * 4);
+  }
+  /* W1 and W3 rows interleaved per layer. */
+  std::vector<int8_t> w13(L * 2 * H * D);
+  std::vector<float> s13(L * 2 * H);
+  for (size_t l = 0; l < L; ++l) {
+    for (size_t r = 0; r < H; ++r) {
+      memcpy(&w13[(l * 2 * H + 2 * r) * D], w->w1_q + (l * H + r) * D, D);
+      memcpy(&w13[(l * 2 * H + 2 * r + 1) * D], w->w3_q + (l * H + r) * D, D);
+      s13[l * 2 * H + 2 * r] = w->w1_s[l * H + r];
+      s13[l * 2 * H + 2 * r + 1] = w->w3_s[l * H + r];
+    }
+  }
+  m->wqkv = upload(*m, qkv.data(), qkv.size());
+  m->sqkv = upload(*m, sqkv.data(), sqkv.size());
+  m->w13 = upload(*m, w13.data(), w13.size());
+  m->s13 = upload(*m, s13.data(), s13.size());
+  m->wo = upload(*m, w->wo_q, L * D * D);
+  m->so = upload(*m, w->wo_s, L * D);
+  m->w2 = upload(*m, w->w2_q, L * D * H);
+  m->s2 = upload(*m, w->w2_s, L * D);
+  m->tok_q = upload(*m, w->tok_q, (size_t)c.vocab_size * D);
+  m->tok_s = upload(*m, w->tok_s, (size_t)c.vocab_size);
+  m->rms_att = upload(*m, w->rms_att, L * D);
+  m->rms_ffn = upload(*m, w->rms_ffn, L * D);
+  m->rms_final = upload(*m, w->rms_final, D);
+  m->rope = upload(*m, w->rope, (size_t)c.seq_len * hs);
+  m->kcache = alloc<float>(*m, L * (size_t)c.seq_len * KV);
+  m->vcache = alloc<float>(*m, L * (size_t)c.seq_len * KV);
+  m->x = alloc<float>(*m, D);
+  m->q = alloc<float>(*m, D);
+  m->logits = alloc<float>(*m, (size_t)c.vocab_size);
+  m->att16 = alloc<uint16_t>(*m, D);
+  m->hb16 = alloc<uint16_t>(*m, H);
+  m->pos = alloc<int>(*m, 1);
+  VX_HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  return m;
+}
+
+int32_t vx_llama_i8_generate(void *model, const int32_t *prompt,
+                             int32_t n_prompt, int32_t n_steps,
+                             int32_t *out_tokens, float *out_margin,
+                             int32_t flags) {
+  LlamaI8 *m = static_cast<LlamaI8 *>(model);
+  if (!m || !prompt || !out_tokens || n_prompt < 1 || n_steps < 1) {
+    return refuse(VX_OP_EINVAL, "need a model, a prompt of at least one "
+                                "token and at least one step");
+  }
+  if (n_prompt + n_steps - 1 > m->cfg.seq_len) {
+    return refuse(VX_OP_EINVAL, "prompt + steps exceed the model's seq_len");
+  }
+  for (int i = 0; i < n_prompt; ++i) {
+    if (prompt[i] < 0 || prompt[i] >= m->cfg.vocab_size) {
+      return refuse(VX_OP_EINVAL, "a prompt token is outside the vocabulary");
+    }
+  }
+  VX_HIP_CHECK(hipSetDevice(m->device));
+  ensure_io(*m, n_prompt, n_steps);
+  VX_HIP_CHECK(hipMemcpyAsync(m->prompt, prompt, sizeof(int) * n_prompt,
+                              hipMemcpyHostToDevice, m->stream));
+  vxk::StepArgmaxArgs start = argmax_args(*m, n_prompt);
+  vxk::step_start_launch(start, m->stream);
+  const int positions = n_prompt + n_steps - 1;
+  if (flags & VX_LLAMA_GRAPH) {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    VX_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+    enqueue_step(*m, n_prompt);
+    VX_HIP_CHECK(hipStreamEndCapture(m->stream, &graph));
+    VX_HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    for (int p = 0; p < positions; ++p) {
+      VX_HIP_CHECK(hipGraphLaunch(exec, m->stream));
+    }
+    VX_HIP_CHECK(hipStreamSynchronize(m->stream));
+    VX_HIP_CHECK(hipGraphExecDestroy(exec));
+    VX_HIP_CHECK(hipGraphDestroy(graph));
+  } else {
+    for (int p = 0; p < positions; ++p) {
+      enqueue_step(*m, n_prompt);
+    }
+  }
+  VX_HIP_CHECK(hipGetLastError());
+  VX_HIP_CHECK(hipMemcpyAsync(out_tokens, m->out_tokens,
+                              sizeof(int) * n_steps, hipMemcpyDeviceToHost,
+                              m->stream));
+  if (out_margin) {
+    VX_HIP_CHECK(hipMemcpyAsync(out_margin, m->out_margin,
+                                sizeof(float) * n_steps,
+                                hipMemcpyDeviceToHost, m->stream));
+  }
+  VX_HIP_CHECK(hipStreamSynchronize(m->stream));
+  return VX_OP_OK;
+}
+
+int32_t vx_llama_i8_logits(void *model, const int32_t *tokens, int32_t n,
+                           float *logits) {
+  LlamaI8 *m = static_cast<LlamaI8 *>(model);
+  if (!m || !tokens || !logits || n < 1 || n > m->cfg.seq_len) {
+    return refuse(VX_OP_EINVAL, "need a model, 1..seq_len tokens and an "
+                                "output buffer");
+  }
+  for (int i = 0; i < n; ++i) {
+    if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size) {
+      return refuse(VX_OP_EINVAL, "a token is outside the vocabulary");
+    }
+  }
+  VX_HIP_CHECK(hipSetDevice(m->device));
+  ensure_io(*m, n, 1);
+  VX_HIP_CHECK(hipMemcpyAsync(m->prompt, tokens, sizeof(int) * n,
+                              hipMemcpyHostToDevice, m->stream));
+  vxk::step_start_launch(argmax_args(*m, n), m->stream);
+  const size_t vocab = (size_t)m->cfg.vocab_size;
+  for (int p = 0; p < n; ++p) {
+    enqueue_step(*m, n);
+    VX_HIP_CHECK(hipMemcpyAsync(logits + p * vocab, m->logits,
+                                sizeof(float) * vocab, hipMemcpyDeviceToHost,
+                                m->stream));
+  }
+  VX_HIP_CHECK(hipStreamSynchronize(m->stream));
+  return VX_OP_OK;
+}
+
+void vx_llama_i8_destroy(void *model) {
+  LlamaI8 *m = static_cast<LlamaI8 *>(model);
+  if (!m) {
+    return;
+  }
+  (void)hipSetDevice(m->device);
+  release(*m);
+  delete m;
+}
+
+} // extern "C"

@@ -1,0 +1,67 @@
+/*
+ * vx_decode_kernels.h -- launchers of the decode-step kernels
+ * (kernels/decode.hip), driven by decode.cpp. Every pointer is device
+ * memory; `pos` is the device-resident position of the step.
+ */
+#ifndef VX_AMD_DECODE_KERNELS_H
+#define VX_AMD_DECODE_KERNELS_H
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vxk {
+
+struct StepGemvArgs {
+  const int8_t *w;     /* [rows, cols] */
+  const float *scale;  /* [rows] */
+  int rows, cols;
+  const float *x;      /* residual stream, normalised on the way in */
+  const float *norm;   /* RMSNorm weight */
+  const uint16_t *in16; /* bf16 input (residual mode) */
+  float *out;          /* q, x (accumulated) or logits */
+  uint16_t *out16;     /* SwiGLU output */
+  float *kcache, *vcache; /* this layer's [seq, kv_dim] */
+  const float *rope;   /* [seq, hs/2, 2] */
+  const int *pos;
+  int dim, kv_dim, hs;
+};
+
+struct StepAttnArgs {
+  const float *q;
+  const float *kcache, *vcache;
+  uint16_t *att16;
+  const int *pos;
+  int kv_dim, hs, kv_mul;
+};
+
+struct StepArgmaxArgs {
+  const float *logits;
+  int vocab;
+  int *pos;
+  const int *prompt;
+  int n_prompt;
+  int *out_tokens;
+  float *out_margin;
+  int out_cap;
+  const int8_t *tok_q;
+  const float *tok_s;
+  float *x;
+  int dim;
+};
+
+/* rows even, cols a multiple of 16 and at most 4096. */
+bool step_gemv_ok(int rows, int cols);
+void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s);
+void step_gemv_resid(const StepGemvArgs &a, hipStream_t s);
+void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s);
+void step_gemv_logits(const StepGemvArgs &a, hipStream_t s);
+/* hs divides 256 and is at most 256; seq_len * 4 bytes of LDS. */
+void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
+                           hipStream_t s);
+void step_argmax_launch(const StepArgmaxArgs &a, hipStream_t s);
+void step_start_launch(const StepArgmaxArgs &a, hipStream_t s);
+
+} // namespace vxk
+
+#endif /* VX_AMD_DECODE_KERNELS_H */

@@ -64,6 +64,10 @@ HIP_SIGNATURES = {
     "vx_nn_flash_attention_fwd_bf16": (
         _i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _i32]),
     "vx_nn_gemv_i8_bf16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64]),
+    "vx_llama_i8_create": (_vp, [_vp, _vp, _u32]),
+    "vx_llama_i8_generate": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _i32]),
+    "vx_llama_i8_logits": (_i32, [_vp, _vp, _i32, _vp]),
+    "vx_llama_i8_destroy": (None, [_vp]),
 }
 
 
