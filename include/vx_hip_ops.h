@@ -69,8 +69,8 @@ int32_t vx_nn_gemv_i8_bf16(const int8_t *w, const float *scale,
  * Q/K/V, RoPE, KV cache, causal attention, Wo, SwiGLU FFN, residuals, final
  * RMSNorm, classifier sharing the embedding table, argmax with the lowest
  * index winning a tie) as GPU library ops: every linear is an int8
- * weight-only GEMV with per-row f32 scales whose input is rounded to bf16;
- * everything else is f32. The position and the next token stay on the GPU,
+ * weight-only GEMV with per-row f32 scales; activations and everything else
+ * are f32, as in the reference. The position and the next token stay on the GPU,
  * so a whole step is replayable as one hipGraph with no host round trip.
  *
  * Weights are host pointers in llama2.c order, matrices [out][in]:

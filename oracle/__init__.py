@@ -55,6 +55,7 @@ def lib() -> ctypes.CDLL:
                                                 ctypes.c_double, _i32, _p, _i64, _p, _p]),
             "vx_oracle_gemv_i8": (None, [_p, _p, _p, _p, _i64, _i64, _i64]),
             "vx_oracle_gemv_i8_f64": (None, [_p, _p, _p, _p, _i64, _i64, _i64]),
+            "vx_oracle_gemv_i8_f32in": (None, [_p, _p, _p, _p, _i64, _i64]),
             "vx_oracle_quantize_rows": (None, [_p, _i64, _i64, _p, _p]),
             "vx_oracle_llama_generate": (_i32, [ctypes.POINTER(LlamaConfig), ctypes.POINTER(LlamaWeights),
                                                 _p, _i32, _i32, _p, _p]),
@@ -160,6 +161,15 @@ def gemv_i8_f64(w, scale, x16) -> np.ndarray:
     y = np.empty((batch, rows), np.float64)
     lib().vx_oracle_gemv_i8_f64(w.ctypes.data, scale.ctypes.data, x16.ctypes.data, y.ctypes.data,
                                 rows, cols, batch)
+    return y
+
+
+def gemv_i8_f32in(w, scale, x) -> np.ndarray:
+    w, scale, x = _c(w, np.int8), _c(scale, np.float32), _c(x, np.float32)
+    rows, cols = w.shape
+    y = np.empty(rows, np.float32)
+    lib().vx_oracle_gemv_i8_f32in(w.ctypes.data, scale.ctypes.data, x.ctypes.data, y.ctypes.data,
+                                  rows, cols)
     return y
 
 

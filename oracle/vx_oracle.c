@@ -27,6 +27,8 @@
  *  - gemv_i8 / gemv_i8_f64: numpy int64 exact dot for integer x; f64 matrix
  *    product otherwise.
  *  - quantize_rows: numpy round-half-even; the extremes map to +-127.
+ *  - gemv_i8_f32in: numpy f64 matrix product (f32-activation form the
+ *    decode uses).
  *  - llama_forward / llama_generate: a vectorised numpy restatement of
  *    examples/llama.vx on a tiny config, position by position (logits within
  *    f32 tolerance, identical tokens).
@@ -232,6 +234,20 @@ void vx_oracle_gemv_i8_f64(const int8_t *w, const float *scale,
   }
 }
 
+void vx_oracle_gemv_i8_f32in(const int8_t *w, const float *scale,
+                             const float *x, float *y, int64_t rows,
+                             int64_t cols) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const int8_t *wr = w + r * cols;
+    float acc = 0.0f;
+    for (int64_t c = 0; c < cols; ++c) {
+      float prod = (float)wr[c] * x[c];
+      acc = acc + prod;
+    }
+    y[r] = scale[r] * acc;
+  }
+}
+
 void vx_oracle_quantize_rows(const float *w, int64_t rows, int64_t cols,
                              int8_t *q, float *scale) {
   for (int64_t r = 0; r < rows; ++r) {
@@ -273,12 +289,6 @@ static void rmsnorm(float *o, const float *x, const float *weight, int size) {
   }
 }
 
-static void round_bf16(const float *x, uint16_t *out, int n) {
-  for (int i = 0; i < n; ++i) {
-    out[i] = vx_oracle_f32_to_bf16(x[i]);
-  }
-}
-
 void vx_oracle_llama_forward(const vx_llama_config *cfg,
                              const vx_llama_weights *w, float *kv,
                              int32_t token, int32_t pos, float *logits) {
@@ -298,7 +308,6 @@ void vx_oracle_llama_forward(const vx_llama_config *cfg,
   float *vv = (float *)malloc(sizeof(float) * kv_dim);
   float *h1 = (float *)malloc(sizeof(float) * hidden);
   float *h3 = (float *)malloc(sizeof(float) * hidden);
-  uint16_t *act = (uint16_t *)malloc(sizeof(uint16_t) * (hidden > dim ? hidden : dim));
 
   /* 1. Embedding: the int8 row times its scale (reference
    * examples/llama.vx:182-185 reads the f32 table). */
@@ -309,15 +318,14 @@ void vx_oracle_llama_forward(const vx_llama_config *cfg,
   for (int l = 0; l < cfg->n_layers; ++l) {
     /* 2.1 attention RMSNorm */
     rmsnorm(xb, x, w->rms_att + (int64_t)l * dim, dim);
-    /* 2.2 Q, K, V: the int8 GEMV of the bf16-rounded activations
-     * (reference :191-233 uses f32 `@` with M = 1). */
-    round_bf16(xb, act, dim);
-    vx_oracle_gemv_i8(w->wq_q + (int64_t)l * dim * dim, w->wq_s + (int64_t)l * dim,
-                      act, q, dim, dim, 1);
-    vx_oracle_gemv_i8(w->wk_q + (int64_t)l * kv_dim * dim,
-                      w->wk_s + (int64_t)l * kv_dim, act, kk, kv_dim, dim, 1);
-    vx_oracle_gemv_i8(w->wv_q + (int64_t)l * kv_dim * dim,
-                      w->wv_s + (int64_t)l * kv_dim, act, vv, kv_dim, dim, 1);
+    /* 2.2 Q, K, V: int8 weights, f32 activations (reference :191-233 is the
+     * f32 `@` with M = 1). */
+    vx_oracle_gemv_i8_f32in(w->wq_q + (int64_t)l * dim * dim,
+                            w->wq_s + (int64_t)l * dim, xb, q, dim, dim);
+    vx_oracle_gemv_i8_f32in(w->wk_q + (int64_t)l * kv_dim * dim,
+                            w->wk_s + (int64_t)l * kv_dim, xb, kk, kv_dim, dim);
+    vx_oracle_gemv_i8_f32in(w->wv_q + (int64_t)l * kv_dim * dim,
+                            w->wv_s + (int64_t)l * kv_dim, xb, vv, kv_dim, dim);
     /* 2.3 RoPE on (even, odd) pairs (reference :235-264); the angle's cos and
      * sin come from the shared table. */
     for (int i = 0; i < dim; i += 2) {
@@ -373,19 +381,17 @@ void vx_oracle_llama_forward(const vx_llama_config *cfg,
       }
     }
     /* 2.6 output projection and residual (reference :327-344) */
-    round_bf16(xb, act, dim);
-    vx_oracle_gemv_i8(w->wo_q + (int64_t)l * dim * dim, w->wo_s + (int64_t)l * dim,
-                      act, xb2, dim, dim, 1);
+    vx_oracle_gemv_i8_f32in(w->wo_q + (int64_t)l * dim * dim,
+                            w->wo_s + (int64_t)l * dim, xb, xb2, dim, dim);
     for (int i = 0; i < dim; ++i) {
       x[i] = x[i] + xb2[i];
     }
     /* 2.7-2.8 FFN RMSNorm, W1/W3, SwiGLU, W2, residual (reference :346-395) */
     rmsnorm(xb, x, w->rms_ffn + (int64_t)l * dim, dim);
-    round_bf16(xb, act, dim);
-    vx_oracle_gemv_i8(w->w1_q + (int64_t)l * hidden * dim,
-                      w->w1_s + (int64_t)l * hidden, act, h1, hidden, dim, 1);
-    vx_oracle_gemv_i8(w->w3_q + (int64_t)l * hidden * dim,
-                      w->w3_s + (int64_t)l * hidden, act, h3, hidden, dim, 1);
+    vx_oracle_gemv_i8_f32in(w->w1_q + (int64_t)l * hidden * dim,
+                            w->w1_s + (int64_t)l * hidden, xb, h1, hidden, dim);
+    vx_oracle_gemv_i8_f32in(w->w3_q + (int64_t)l * hidden * dim,
+                            w->w3_s + (int64_t)l * hidden, xb, h3, hidden, dim);
     for (int i = 0; i < hidden; ++i) {
       float val = h1[i];
       float neg = 0.0f - val;
@@ -393,17 +399,15 @@ void vx_oracle_llama_forward(const vx_llama_config *cfg,
       val = val * h3[i];
       h1[i] = val;
     }
-    round_bf16(h1, act, hidden);
-    vx_oracle_gemv_i8(w->w2_q + (int64_t)l * dim * hidden, w->w2_s + (int64_t)l * dim,
-                      act, xb, dim, hidden, 1);
+    vx_oracle_gemv_i8_f32in(w->w2_q + (int64_t)l * dim * hidden,
+                            w->w2_s + (int64_t)l * dim, h1, xb, dim, hidden);
     for (int i = 0; i < dim; ++i) {
       x[i] = x[i] + xb[i];
     }
   }
   /* 3-4. final RMSNorm in place, classifier (reference :397-417) */
   rmsnorm(x, x, w->rms_final, dim);
-  round_bf16(x, act, dim);
-  vx_oracle_gemv_i8(w->tok_q, w->tok_s, act, logits, cfg->vocab_size, dim, 1);
+  vx_oracle_gemv_i8_f32in(w->tok_q, w->tok_s, x, logits, cfg->vocab_size, dim);
 
   free(x);
   free(xb);
@@ -413,7 +417,6 @@ void vx_oracle_llama_forward(const vx_llama_config *cfg,
   free(vv);
   free(h1);
   free(h3);
-  free(act);
 }
 
 int32_t vx_oracle_llama_generate(const vx_llama_config *cfg,

@@ -73,6 +73,13 @@ void vx_oracle_gemv_i8_f64(const int8_t *w, const float *scale,
                            const uint16_t *x, double *y, int64_t rows,
                            int64_t cols, int64_t batch);
 
+/* y[r] = scale[r] * sum_c w[r, c] * x[c] with an f32 activation vector:
+ * the weight-only int8 linear of the decode step (activations stay f32, as
+ * in reference examples/llama.vx). */
+void vx_oracle_gemv_i8_f32in(const int8_t *w, const float *scale,
+                             const float *x, float *y, int64_t rows,
+                             int64_t cols);
+
 /* Per-output-row symmetric int8 quantization: scale = max|w| / 127 (1 for an
  * all-zero row), q = round-half-even(w / scale) clamped to [-127, 127]. */
 void vx_oracle_quantize_rows(const float *w, int64_t rows, int64_t cols,
@@ -112,8 +119,9 @@ typedef struct {
  * tokens to out_tokens[n_steps] and, per generated token, the gap between
  * the best and the second-best logit to out_margin (may be NULL). Returns 0,
  * or -1 when the arguments do not fit the config. Follows reference
- * examples/llama.vx:145-420 with the int8/bf16 points of
- * vx_llama_forward. */
+ * examples/llama.vx:145-420 with int8 weights (per-row scales) and f32
+ * activations; the embedding is the int8 row times its scale and the
+ * RoPE angles come from the `rope` table. */
 int32_t vx_oracle_llama_generate(const vx_llama_config *cfg,
                                  const vx_llama_weights *w,
                                  const int32_t *prompt, int32_t n_prompt,

@@ -54,8 +54,8 @@ def gemm_bf16_linalg(a16, b16) -> np.ndarray:
 
 def llama_logits(cfg, model: dict, tokens) -> list[np.ndarray]:
     """Logits after each of `tokens` fed at positions 0.., restating
-    reference examples/llama.vx:173-420 with the int8 weights, bf16-rounded
-    GEMV inputs and the shared RoPE table."""
+    reference examples/llama.vx:173-420 with the int8 weights (f32
+    activations) and the shared RoPE table."""
     d, hd, L = cfg.dim, cfg.hidden_dim, cfg.n_layers
     hs, kvd = cfg.head_size, cfg.kv_dim
     kv_mul = cfg.n_heads // cfg.n_kv_heads
@@ -63,7 +63,7 @@ def llama_logits(cfg, model: dict, tokens) -> list[np.ndarray]:
     vc = np.zeros((L, cfg.seq_len, kvd), np.float32)
 
     def gemv(q, s, x):
-        xb = bf16_round(x).astype(np.float64)
+        xb = np.asarray(x, np.float32).astype(np.float64)
         return (s.astype(np.float64) * (q.astype(np.float64) @ xb)).astype(np.float32)
 
     def rms(x, w):

@@ -246,6 +246,18 @@ def test_oracle_gemv_close_to_f64(rng):
     np.testing.assert_allclose(y, want, rtol=1e-4, atol=1e-4)
 
 
+def test_oracle_gemv_f32_input(rng):
+    w = rng.integers(-127, 128, (80, 768), dtype=np.int8)
+    x = rng.standard_normal(768).astype(np.float32)
+    s = rng.uniform(0.001, 0.01, 80).astype(np.float32)
+    y = oracle.gemv_i8_f32in(w, s, x)
+    want = s.astype(np.float64) * (w.astype(np.float64) @ x.astype(np.float64))
+    np.testing.assert_allclose(y, want, rtol=1e-5, atol=1e-6)
+    xi = rng.integers(-8, 9, 768).astype(np.float32)  # exact sums
+    assert np.array_equal(oracle.gemv_i8_f32in(w, s, xi),
+                          s * (w.astype(np.int64) @ xi.astype(np.int64)).astype(np.float32))
+
+
 def test_quantize_matches_package(rng):
     w = rng.standard_normal((33, 77)).astype(np.float32) * 0.02
     w[3] = 0.0
@@ -268,7 +280,7 @@ def test_oracle_llama_matches_numpy_tiny():
     want = npr.llama_logits(cfg, model, tokens)
     for pos, tok in enumerate(tokens):
         got = oracle.llama_forward(cfg.as_dict(), model, kv, int(tok), pos)
-        np.testing.assert_allclose(got, want[pos], rtol=2e-3, atol=2e-4)
+        np.testing.assert_allclose(got, want[pos], rtol=1e-4, atol=1e-5)
 
 
 def test_oracle_llama_generate_greedy_is_argmax_chain():

@@ -32,7 +32,7 @@ struct LlamaI8 {
         *rope = nullptr;
   float *kcache = nullptr, *vcache = nullptr;
   float *x = nullptr, *q = nullptr, *logits = nullptr;
-  uint16_t *att16 = nullptr, *hb16 = nullptr;
+  float *att = nullptr, *hb = nullptr;
   int *pos = nullptr, *prompt = nullptr, *out_tokens = nullptr;
   float *out_margin = nullptr;
   int prompt_cap = 0, out_cap = 0;
@@ -129,7 +129,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     at.q = m.q;
     at.kcache = g.kcache;
     at.vcache = g.vcache;
-    at.att16 = m.att16;
+    at.att = m.att;
     at.pos = m.pos;
     at.kv_dim = m.kv_dim;
     at.hs = m.hs;
@@ -141,7 +141,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     wo.scale = m.so + (int64_t)l * c.dim;
     wo.rows = c.dim;
     wo.cols = c.dim;
-    wo.in16 = m.att16;
+    wo.in = m.att;
     wo.out = m.x;
     vxk::step_gemv_resid(wo, m.stream);
 
@@ -152,7 +152,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     ffn.cols = c.dim;
     ffn.x = m.x;
     ffn.norm = m.rms_ffn + (int64_t)l * c.dim;
-    ffn.out16 = m.hb16;
+    ffn.hout = m.hb;
     vxk::step_gemv_swiglu(ffn, m.stream);
 
     vxk::StepGemvArgs w2 = g;
@@ -160,7 +160,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     w2.scale = m.s2 + (int64_t)l * c.dim;
     w2.rows = c.dim;
     w2.cols = c.hidden_dim;
-    w2.in16 = m.hb16;
+    w2.in = m.hb;
     w2.out = m.x;
     vxk::step_gemv_resid(w2, m.stream);
   }
@@ -271,8 +271,8 @@ void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
   m->x = alloc<float>(*m, D);
   m->q = alloc<float>(*m, D);
   m->logits = alloc<float>(*m, (size_t)c.vocab_size);
-  m->att16 = alloc<uint16_t>(*m, D);
-  m->hb16 = alloc<uint16_t>(*m, H);
+  m->att = alloc<float>(*m, D);
+  m->hb = alloc<float>(*m, H);
   m->pos = alloc<int>(*m, 1);
   VX_HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
   return m;

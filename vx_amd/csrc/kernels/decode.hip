@@ -5,20 +5,21 @@
  * A step is 5 launches per layer plus 2, each reading the position from
  * device memory so that a captured step replays unchanged:
  *
- *   step_gemv<kQkv>    RMSNorm(x) -> bf16, [Wq; Wk; Wv] int8 GEMV, RoPE on
+ *   step_gemv<kQkv>    RMSNorm(x), [Wq; Wk; Wv] int8 GEMV, RoPE on
  *                      q and k, k and v into the KV cache at `pos`
  *   step_attention     one workgroup per head: softmax(q k^T / sqrt(hs)) v
- *                      over positions 0..pos -> bf16
+ *                      over positions 0..pos
  *   step_gemv<kResid>  x += Wo att
- *   step_gemv<kSwiglu> RMSNorm(x) -> bf16, [W1; W3] GEMV with rows
- *                      interleaved, silu(h1) * h3 -> bf16
+ *   step_gemv<kSwiglu> RMSNorm(x), [W1; W3] GEMV with rows interleaved,
+ *                      silu(h1) * h3
  *   step_gemv<kResid>  x += W2 h
  *   step_gemv<kLogits> final RMSNorm, classifier (the embedding table)
  *   step_argmax        argmax (lowest index wins a tie) or the next prompt
  *                      token; x = embedding of that token; pos += 1
  *
- * Every GEMV is weight-only int8 with one f32 scale per row, input rounded
- * to bf16, f32 sums; each wave owns two adjacent rows, so the even/odd RoPE
+ * Every GEMV is weight-only int8 with one f32 scale per row over f32
+ * activations (as in the reference, which is f32 throughout), f32 sums;
+ * each wave owns two adjacent rows, so the even/odd RoPE
  * pair and the (h1, h3) SwiGLU pair finish in one lane. Contraction is off
  * so the elementwise arithmetic rounds where the reference's f32 loop nest
  * rounds; only the summation order differs.
@@ -83,10 +84,6 @@ __device__ float block_max(float v, float *scratch) {
   return t;
 }
 
-__device__ __forceinline__ float round_bf16(float x) {
-  return bf16_to_f32(f32_to_bf16(x));
-}
-
 enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3 };
 
 template <int kMode>
@@ -98,10 +95,10 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   const int cols = a.cols;
   if constexpr (kMode == kResid) {
     for (int i = t; i < cols; i += kThreads) {
-      xin[i] = bf16_to_f32(a.in16[i]);
+      xin[i] = a.in[i];
     }
   } else {
-    /* RMSNorm as reference examples/llama.vx:145-158, rounded to bf16. */
+    /* RMSNorm as reference examples/llama.vx:145-158. */
     float ss = 0.0f;
     for (int i = t; i < cols; i += kThreads) {
       const float v = a.x[i];
@@ -110,7 +107,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     ss = block_sum(ss, scratch);
     const float inv = 1.0f / sqrtf(ss / (float)cols + 0.00001f);
     for (int i = t; i < cols; i += kThreads) {
-      xin[i] = round_bf16(a.norm[i] * (inv * a.x[i]));
+      xin[i] = a.norm[i] * (inv * a.x[i]);
     }
   }
   __syncthreads();
@@ -175,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     const float neg = 0.0f - val;
     val = val * (1.0f / (1.0f + expf(neg)));
     val = val * y1;
-    a.out16[r0 >> 1] = f32_to_bf16(val);
+    a.hout[r0 >> 1] = val;
   } else {
     a.out[r0] = y0;
     a.out[r0 + 1] = y1;
@@ -237,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
       o += part[gg * hs + t];
     }
     const float inv = 1.0f / sum;
-    a.att16[h * hs + t] = f32_to_bf16(o * inv);
+    a.att[h * hs + t] = o * inv;
   }
 }
 

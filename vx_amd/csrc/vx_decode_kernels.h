@@ -18,9 +18,9 @@ struct StepGemvArgs {
   int rows, cols;
   const float *x;      /* residual stream, normalised on the way in */
   const float *norm;   /* RMSNorm weight */
-  const uint16_t *in16; /* bf16 input (residual mode) */
+  const float *in;     /* input vector (residual mode) */
   float *out;          /* q, x (accumulated) or logits */
-  uint16_t *out16;     /* SwiGLU output */
+  float *hout;         /* SwiGLU output */
   float *kcache, *vcache; /* this layer's [seq, kv_dim] */
   const float *rope;   /* [seq, hs/2, 2] */
   const int *pos;
@@ -30,7 +30,7 @@ struct StepGemvArgs {
 struct StepAttnArgs {
   const float *q;
   const float *kcache, *vcache;
-  uint16_t *att16;
+  float *att;
   const int *pos;
   int kv_dim, hs, kv_mul;
 };
