@@ -248,11 +248,12 @@ def test_mfma_variants_bit_identical(hiplib, out_dt, rng):
     a16 = f32_to_bf16(rng.normal(0, 1, (512, 768)).astype(np.float32))
     b16 = f32_to_bf16(rng.normal(0, 1, (768, 1024)).astype(np.float32))
     outs = []
-    for kern in (abi.GEMM_MFMA, abi.GEMM_MFMA_PIPE4, abi.GEMM_MFMA_PIPE8):
+    for kern in (abi.GEMM_MFMA, abi.GEMM_MFMA_PIPE4, abi.GEMM_MFMA_PIPE8, abi.GEMM_MFMA_IL,
+                 abi.GEMM_MFMA_DMA, abi.GEMM_MFMA_DMA8):
         c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, out_dt, kernel=kern)
         assert st["gemm_mfma"] == 1
         outs.append(c)
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
     want = oracle.gemm_bf16_f32(a16, b16)
     if out_dt == abi.DTYPE_F32:
         assert_max_abs(outs[0], want, 1e-3, "variants vs oracle")

@@ -725,9 +725,11 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   }
   case VX_HIP_CTRL_GEMM_KERNEL: {
     /* payload -> int32_t: 0 automatic, 1 MFMA (plain), 2 tiled, 3 MFMA
-     * pipelined on 4 waves, 4 MFMA pipelined on 8 waves. */
+     * pipelined on 4 waves, 4 MFMA pipelined on 8 waves, 5 MFMA with the
+     * non-MFMA work interleaved, 6/7 MFMA with direct-to-LDS loads (4 or 8
+     * waves). */
     const int32_t *which = static_cast<const int32_t *>(payload);
-    if (!which || *which < 0 || *which > 4) {
+    if (!which || *which < 0 || *which > 7) {
       return 0;
     }
     forced_gemm_kernel.store(*which);

@@ -404,6 +404,503 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN, 1) void gemm_mfma_pipe(
   }
 }
 
+/* Direct-to-LDS variant for gfx950: the same 256x256 tile and wave layout,
+ * K walked in stages of 32 through a ring of kDmaStages LDS slots (32 KiB
+ * each).
+ *
+ * Global data goes straight into LDS (buffer_load_dwordx4 ... lds): lane i of
+ * a load writes the 16 bytes at LDS base + 16*i, so each lane fetches the
+ * global 16 bytes that belong at its LDS slot. No staging registers, no LDS
+ * write instructions, and a stage's loads are issued three stages before the
+ * stage is consumed.
+ *
+ * A's plane is row-major [256 rows][4 chunks of 8 k], chunk index XORed with
+ * bits 1-2 of the row so a ds_read_b128 of 16 rows at one chunk covers all
+ * (row mod 4, chunk) bank slots. B's plane keeps global order, [32 k][256 n]
+ * in 16-byte chunks with the chunk index XORed by a function of k mod 4; its
+ * MFMA operand (8 consecutive k per lane) comes from two ds_read_b64_tr_b16,
+ * which, within each group of 16 lanes, hands lane j element j%4 of the
+ * 8 bytes read by lane 4e + j/4 as its element e: lanes 4e..4e+3 read row
+ * k+e, 4 columns each, and lane j receives column j of rows k..k+3.
+ *
+ * The buffer descriptors bound each load to the operand's extent, so an
+ * offset past it reads zeros instead of faulting. */
+constexpr int kDStageK = 32;
+#ifndef VX_GEMM_DMA_STAGES
+#define VX_GEMM_DMA_STAGES 4
+#endif
+constexpr int kDmaStages = VX_GEMM_DMA_STAGES; /* LDS ring depth */
+constexpr int kDUnits = kTileM * kDStageK / 8; /* 16-byte units per plane */
+constexpr int kBufferFlags = 0x00020000;       /* raw 32-bit dwords */
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define VX_LDS __attribute__((address_space(3)))
+
+__device__ __forceinline__ int dswz_a(int row, int c) {
+  return c ^ (((row >> 1) ^ (row >> 2)) & 3);
+}
+
+__device__ __forceinline__ int dswz_b(int k, int c) {
+  const int q = k & 3;
+  return c ^ ((q << 1) ^ (q << 2));
+}
+
+/* Wait until at most `n` of this wave's vector memory operations are
+ * outstanding (vmcnt n; lgkmcnt and expcnt untouched). */
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+/* Wait until at most `newer` (0..kMax) whole stages of this wave's loads are
+ * outstanding; each stage is kPer loads. */
+template <int kMax, int kPer>
+__device__ __forceinline__ void wait_stages(int newer) {
+  if constexpr (kMax >= 3) {
+    if (newer >= 3) {
+      wait_vm<3 * kPer>();
+      return;
+    }
+  }
+  if constexpr (kMax >= 2) {
+    if (newer >= 2) {
+      wait_vm<2 * kPer>();
+      return;
+    }
+  }
+  if constexpr (kMax >= 1) {
+    if (newer >= 1) {
+      wait_vm<kPer>();
+      return;
+    }
+  }
+  wait_vm<0>();
+}
+
+/* One 16-byte-per-lane load from the buffer `rsrc` at byte offset `voff`
+ * into LDS at `lds` + 16*lane. Written as assembly so the compiler neither
+ * waits for it at every LDS read (it cannot tell which ring slot the load
+ * fills) nor drops the barrier-time vmcnt(0) it adds for a fenced barrier:
+ * the kernel orders these loads itself with wait_vm and lds_barrier. The
+ * nop covers the one wait state between the M0 write and its use. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm" /* m0 is reserved: declared */
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+/* Workgroup barrier without the release fence __syncthreads carries (that
+ * fence waits for every outstanding global load, the prefetches included).
+ * LDS reads are drained first so a slot is never refilled under a reader. */
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0) */
+  asm volatile("s_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ i32x4 buffer_rsrc(const void *base, int bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu); /* stride 0 */
+  r[2] = bytes;
+  r[3] = kBufferFlags;
+  return r;
+}
+
+template <int kWM, int kWN, int kNS, bool kBf16, int kOut>
+__global__ __launch_bounds__(64 * kWM * kWN, 1) void gemm_mfma_dma(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
+    int tiles_m, int tiles_n) {
+  constexpr int kLoads = kDUnits / 64 / (kWM * kWN); /* per wave per plane */
+  constexpr int kWaveM = kTileM / kWM;                /* rows of C per wave */
+  constexpr int kWaveN = kTileN / kWN;                /* columns per wave */
+  constexpr int kTM = kWaveM / 32;
+  constexpr int kTN = kWaveN / 32;
+  static_assert(kLoads >= 1 && kTM >= 1 && kTN >= 1, "wave grid");
+  static_assert(kNS >= 3 && kNS * 2 * kDUnits * 16 <= 160 * 1024, "LDS ring");
+  __shared__ u32x4 ring[kNS][2][kDUnits];
+
+  const int t = threadIdx.x;
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) {
+    id = (id & 7) * (nwg >> 3) + (id >> 3);
+  }
+  const int group_size = kGroupM * tiles_n;
+  const int first_m = (id / group_size) * kGroupM;
+  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int in_group = id % group_size;
+  const int tm = first_m + in_group % rows_in_group;
+  const int tn = in_group / rows_in_group;
+  const int64_t m0 = (int64_t)tm * kTileM;
+  const int64_t n0 = (int64_t)tn * kTileN;
+
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63;
+
+  /* Byte offsets of this lane's loads, fixed for the whole K walk: load p
+   * of this wave fills units (wave*kLoads + p)*64 + lane of each plane. */
+  uint32_t a_off[kLoads], b_off[kLoads];
+#pragma unroll
+  for (int p = 0; p < kLoads; ++p) {
+    const int u = (wave * kLoads + p) * 64 + lane;
+    const int arow = u >> 2;
+    a_off[p] = (uint32_t)(arow * lda * 2 + dswz_a(arow, u & 3) * 16);
+    const int bk = u >> 5;
+    b_off[p] = (uint32_t)(bk * ldb * 2 + dswz_b(bk, u & 31) * 16);
+  }
+  const int a_bytes = (int)((kTileM - 1) * lda * 2 + kDStageK * 2);
+  const int b_bytes = (int)((kDStageK - 1) * ldb * 2 + kTileN * 2);
+
+  const uint32_t ring_base =
+      (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
+  auto issue = [&](int step, int slot) {
+    const i32x4 ra =
+        buffer_rsrc(A + m0 * lda + (int64_t)step * kDStageK, a_bytes);
+    const i32x4 rb =
+        buffer_rsrc(B + (int64_t)step * kDStageK * ldb + n0, b_bytes);
+    const uint32_t la = ring_base + (uint32_t)(slot * 2 * kDUnits * 16) +
+                        (uint32_t)(wave * kLoads * 64 * 16);
+#pragma unroll
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(ra, a_off[p], la + p * 64 * 16);
+    }
+#pragma unroll
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(rb, b_off[p], la + kDUnits * 16 + p * 64 * 16);
+    }
+  };
+
+  f32x16 acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+      }
+    }
+  }
+
+  const int wm = wave / kWN;
+  const int wn = wave % kWN;
+  const int lrow = lane & 31;
+  const int lk = lane >> 5;
+  /* Transposed B read: group g = lane/16, lane i of the group reads row
+   * k + i/4 at columns 4*(i%4)..+3 of its 16-column half. */
+  const int tr_k = 8 * lk + ((lane & 15) >> 2);
+  const int tr_n = wn * kWaveN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+  /* MFMA operands of k-substep ks of the stage in `slot`. */
+  auto frags = [&](int slot, int ks, u32x4 (&af)[kTM], u32x4 (&bfr)[kTN]) {
+    const u32x4 *la = ring[slot][0];
+    const VX_LDS char *lb = (const VX_LDS char *)&ring[slot][1][0];
+    const int c = ks * 2 + lk;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const int row = wm * kWaveM + i * 32 + lrow;
+      af[i] = la[row * 4 + dswz_a(row, c)];
+    }
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int n = tr_n + j * 32;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = ks * 16 + tr_k + 4 * h;
+        const int at = k * (kTileN * 2) + dswz_b(k, n >> 3) * 16 + (n & 7) * 2;
+        const u32x2 w = __builtin_bit_cast(
+            u32x2,
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS i16x4 *)(lb + at)));
+        bfr[j][2 * h] = w[0];
+        bfr[j][2 * h + 1] = w[1];
+      }
+    }
+  };
+  auto mfmas = [&](const u32x4 (&af)[kTM], const u32x4 (&bfr)[kTN]) {
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) {
+        acc[i][j] = mfma32<kBf16>(af[i], bfr[j], acc[i][j]);
+      }
+    }
+  };
+
+  /* Stage s lives in slot s % kNS. Entering step s, stages up to s + kNS - 2
+   * have been issued and the first substep of stage s is in registers. The
+   * step waits for stage s+1 to land (this wave's loads, then the barrier
+   * for everyone's), refills the slot stage s-1 vacated with stage s+kNS-1,
+   * and reads the first substep of stage s+1 while stage s's second substep
+   * runs on the MFMA pipe. */
+  const int steps = K / kDStageK;
+#pragma unroll
+  for (int s = 0; s < kNS - 1; ++s) {
+    if (s < steps) {
+      issue(s, s);
+    }
+  }
+  wait_stages<kNS - 2, 2 * kLoads>(min(steps - 1, kNS - 2));
+  lds_barrier();
+  u32x4 fa0[kTM], fb0[kTN], fa1[kTM], fb1[kTN];
+  frags(0, 0, fa0, fb0);
+  for (int step = 0; step < steps; ++step) {
+    if (step + 1 < steps) {
+      wait_stages<kNS - 3, 2 * kLoads>(min(steps - 2 - step, kNS - 3));
+    }
+    lds_barrier();
+    if (step + kNS - 1 < steps) {
+      issue(step + kNS - 1, (step + kNS - 1) % kNS);
+    }
+    const int slot = step % kNS;
+    frags(slot, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    /* Unconditional: past the last stage this reads a stale slot nobody
+     * uses, and straight-line code lets the LDS waits stay partial. */
+    frags((step + 1) % kNS, 0, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int64_t col = n0 + wn * kWaveN + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row =
+            m0 + wm * kWaveM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        put<kOut>(C, row * ldc + col, acc[i][j][r]);
+      }
+    }
+  }
+}
+
+/* Interleaved variant: the same tile, the same LDS layout and the same MFMA
+ * order (so bit-identical results), with every non-MFMA instruction of a
+ * stage issued in the shadow of an MFMA. With one wave per SIMD the MFMA
+ * pipe otherwise idles while the wave issues its LDS writes, B transpose,
+ * global loads and address arithmetic between MFMA groups.
+ *
+ * A stage's body is one straight-line block (no branches: the last stages
+ * re-fetch the final K step, in bounds, instead of skipping), split into its
+ * four k-substeps of 16 MFMAs each. Alongside substep 0 the wave reads the
+ * operands of substep 1 and writes its A staging registers into the idle LDS
+ * buffer; alongside substep 1, operands of 2 and the B transpose and write;
+ * alongside 2, operands of 3 and the global loads of A two stages ahead;
+ * alongside 3, those of B. sched_group_barrier fixes the interleave: one
+ * MFMA, then one memory instruction (plus VALU for the transpose). */
+template <bool kBf16, int kOut>
+__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_il(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
+    int tiles_m, int tiles_n) {
+  __shared__ u32x4 lds[2][2][kTileM * kChunks];
+
+  const int t = threadIdx.x;
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) {
+    id = (id & 7) * (nwg >> 3) + (id >> 3);
+  }
+  const int group_size = kGroupM * tiles_n;
+  const int first_m = (id / group_size) * kGroupM;
+  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int in_group = id % group_size;
+  const int tm = first_m + in_group % rows_in_group;
+  const int tn = in_group / rows_in_group;
+  const int64_t m0 = (int64_t)tm * kTileM;
+  const int64_t n0 = (int64_t)tn * kTileN;
+
+  const uint16_t *a_src = A + (m0 + (t >> 3)) * lda + (t & 7) * 8;
+  const int64_t a_pass = 32 * lda;
+  const int kc = t & 7;
+  const int nb = t >> 3;
+  const uint16_t *b_src = B + (int64_t)(kc * 8) * ldb + n0 + nb * 8;
+
+  u32x4 areg[8], breg[8];
+
+  auto fetch_a = [&](int step) {
+    const uint16_t *ap = a_src + (int64_t)step * kStageK;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      areg[p] = *reinterpret_cast<const u32x4 *>(ap + p * a_pass);
+    }
+  };
+  auto fetch_b = [&](int step) {
+    const uint16_t *bp = b_src + (int64_t)step * kStageK * ldb;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      breg[r] = *reinterpret_cast<const u32x4 *>(bp + r * ldb);
+    }
+  };
+  auto stash_a = [&](int s) {
+    u32x4 *la = lds[s][0];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int row = p * 32 + (t >> 3);
+      la[row * kChunks + swz(row, t & 7)] = areg[p];
+    }
+  };
+  auto stash_b = [&](int s) {
+    u32x4 *lb = lds[s][1];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t x = breg[2 * q][w];
+        const uint32_t y = breg[2 * q + 1][w];
+        lo[q] = (x & 0xffffu) | (y << 16);
+        hi[q] = (x >> 16) | (y & 0xffff0000u);
+      }
+      const int row = nb * 8 + 2 * w;
+      lb[row * kChunks + swz(row, kc)] = lo;
+      lb[(row + 1) * kChunks + swz(row + 1, kc)] = hi;
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+      }
+    }
+  }
+
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int lrow = lane & 31;
+  const int lk = lane >> 5;
+
+  u32x4 fa[2][4], fb[2][4];
+  auto frags = [&](int s, int ks, u32x4 *af, u32x4 *bfr) {
+    const u32x4 *la = lds[s][0];
+    const u32x4 *lb = lds[s][1];
+    const int c = ks * 2 + lk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wm * 128 + i * 32 + lrow;
+      af[i] = la[row * kChunks + swz(row, c)];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = wn * 128 + j * 32 + lrow;
+      bfr[j] = lb[row * kChunks + swz(row, c)];
+    }
+  };
+  auto mfmas = [&](const u32x4 *af, const u32x4 *bfr) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = mfma32<kBf16>(af[i], bfr[j], acc[i][j]);
+      }
+    }
+  };
+
+  constexpr int kMfma = 0x008, kValu = 0x002, kVmemRead = 0x020,
+                kDsRead = 0x100, kDsWrite = 0x200;
+
+  const int steps = K / kStageK;
+  fetch_a(0);
+  fetch_b(0);
+  stash_a(0);
+  stash_b(0);
+  fetch_a(min(1, steps - 1));
+  fetch_b(min(1, steps - 1));
+  __syncthreads();
+  for (int step = 0; step < steps; ++step) {
+    const int s = step & 1;
+    const int ahead = min(step + 2, steps - 1);
+    frags(s, 0, fa[0], fb[0]);
+    /* substep 0: operands of 1, A into the idle buffer */
+    frags(s, 1, fa[1], fb[1]);
+    stash_a(s ^ 1);
+    mfmas(fa[0], fb[0]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
+    }
+    /* substep 1: operands of 2, B transposed into the idle buffer */
+    frags(s, 2, fa[0], fb[0]);
+    stash_b(s ^ 1);
+    mfmas(fa[1], fb[1]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
+    }
+    /* substep 2: operands of 3, global loads of A two stages ahead */
+    frags(s, 3, fa[1], fb[1]);
+    fetch_a(ahead);
+    mfmas(fa[0], fb[0]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+    }
+    /* substep 3: global loads of B two stages ahead */
+    fetch_b(ahead);
+    mfmas(fa[1], fb[1]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + wn * 128 + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row =
+            m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        put<kOut>(C, row * ldc + col, acc[i][j][r]);
+      }
+    }
+  }
+}
+
 template <int kIn>
 __device__ __forceinline__ auto load_in(const void *p, int64_t at) {
   if constexpr (kIn == VX_DTYPE_F64) {
@@ -509,6 +1006,14 @@ bool mfma_takes(const GemmArgs &g) {
          g.ldc >= g.n && aligned16(g.a) && aligned16(g.b);
 }
 
+/* The direct-to-LDS kernel addresses a tile's A panel and a stage's B rows
+ * with 32-bit byte offsets from a per-stage base. */
+bool dma_takes(const GemmArgs &g) {
+  return mfma_takes(g) &&
+         (kTileM - 1) * g.lda * 2 + kDStageK * 2 <= INT32_MAX &&
+         (kDStageK - 1) * g.ldb * 2 + kTileN * 2 <= INT32_MAX;
+}
+
 bool tiled_takes(const GemmArgs &g) {
   if (g.m <= 0 || g.n <= 0 || g.k <= 0 || g.lda < g.k || g.ldb < g.n ||
       g.ldc < g.n) {
@@ -561,6 +1066,48 @@ void launch_pipe_any(const GemmArgs &g, hipStream_t s) {
   }
 }
 
+template <bool kBf16, int kOut>
+void launch_il(const GemmArgs &g, hipStream_t s) {
+  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
+  hipLaunchKernelGGL((gemm_mfma_il<kBf16, kOut>), dim3(tiles_m * tiles_n),
+                     dim3(kThreads), 0, s, static_cast<const uint16_t *>(g.a),
+                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
+                     g.ldb, g.ldc, tiles_m, tiles_n);
+}
+
+template <int kWM, int kWN, bool kBf16, int kOut>
+void launch_dma(const GemmArgs &g, hipStream_t s) {
+  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
+  hipLaunchKernelGGL((gemm_mfma_dma<kWM, kWN, kDmaStages, kBf16, kOut>),
+                     dim3(tiles_m * tiles_n), dim3(64 * kWM * kWN), 0, s, static_cast<const uint16_t *>(g.a),
+                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
+                     g.ldb, g.ldc, tiles_m, tiles_n);
+}
+
+template <int kWM, int kWN>
+void launch_dma_any(const GemmArgs &g, hipStream_t s) {
+  const bool bf = g.in_dtype == VX_DTYPE_BF16;
+  if (g.out_dtype == VX_DTYPE_F32) {
+    bf ? launch_dma<kWM, kWN, true, VX_DTYPE_F32>(g, s)
+       : launch_dma<kWM, kWN, false, VX_DTYPE_F32>(g, s);
+  } else if (bf) {
+    launch_dma<kWM, kWN, true, VX_DTYPE_BF16>(g, s);
+  } else {
+    launch_dma<kWM, kWN, false, VX_DTYPE_F16>(g, s);
+  }
+}
+
+void launch_il_any(const GemmArgs &g, hipStream_t s) {
+  const bool bf = g.in_dtype == VX_DTYPE_BF16;
+  if (g.out_dtype == VX_DTYPE_F32) {
+    bf ? launch_il<true, VX_DTYPE_F32>(g, s) : launch_il<false, VX_DTYPE_F32>(g, s);
+  } else if (bf) {
+    launch_il<true, VX_DTYPE_BF16>(g, s);
+  } else {
+    launch_il<false, VX_DTYPE_F16>(g, s);
+  }
+}
+
 template <int kIn, int kOut>
 void launch_tiled(const GemmArgs &g, hipStream_t s) {
   dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((g.m + 63) / 64));
@@ -571,6 +1118,9 @@ void launch_tiled(const GemmArgs &g, hipStream_t s) {
 } // namespace
 
 GemmKernel gemm_pick(const GemmArgs &g) {
+  if (dma_takes(g)) {
+    return GEMM_MFMA_DMA8;
+  }
   if (mfma_takes(g)) {
     return GEMM_MFMA_PIPE4;
   }
@@ -601,6 +1151,21 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
     }
     which == GEMM_MFMA_PIPE4 ? launch_pipe_any<2, 2>(g, stream)
                              : launch_pipe_any<2, 4>(g, stream);
+  } else if (which == GEMM_MFMA_IL) {
+    if (!mfma_takes(g)) {
+      return false;
+    }
+    launch_il_any(g, stream);
+  } else if (which == GEMM_MFMA_DMA) {
+    if (!dma_takes(g)) {
+      return false;
+    }
+    launch_dma_any<2, 2>(g, stream);
+  } else if (which == GEMM_MFMA_DMA8) {
+    if (!dma_takes(g)) {
+      return false;
+    }
+    launch_dma_any<2, 4>(g, stream);
   } else if (which == GEMM_TILED) {
     if (!tiled_takes(g)) {
       return false;

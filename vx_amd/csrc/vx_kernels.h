@@ -34,10 +34,15 @@ enum GemmKernel {
   GEMM_TILED = 2,    /* any supported type, 64x64 tiles, exact k order */
   GEMM_MFMA_PIPE4 = 3, /* as 1, software-pipelined, 4 waves */
   GEMM_MFMA_PIPE8 = 4, /* as 1, software-pipelined, 8 waves */
+  GEMM_MFMA_IL = 5,    /* as 1, every non-MFMA instruction in MFMA shadow */
+  GEMM_MFMA_DMA = 6,   /* as 1, global -> LDS direct, 4-deep ring of K=32 */
+  GEMM_MFMA_DMA8 = 7,  /* as 6, 8 waves (two per SIMD) */
 };
 
 inline bool gemm_is_mfma(GemmKernel k) {
-  return k == GEMM_MFMA_256 || k == GEMM_MFMA_PIPE4 || k == GEMM_MFMA_PIPE8;
+  return k == GEMM_MFMA_256 || k == GEMM_MFMA_PIPE4 || k == GEMM_MFMA_PIPE8 ||
+         k == GEMM_MFMA_IL || k == GEMM_MFMA_DMA ||
+         k == GEMM_MFMA_DMA8;
 }
 
 GemmKernel gemm_pick(const GemmArgs &g);
