@@ -4,137 +4,232 @@
  * y[b, r] = scale[r] * sum_c w[r, c] * x[b, c], w int8 [rows, cols], x bf16
  * [batch, cols], f32 sums.
  *
- * The weights are the traffic: every byte of W is read exactly once, with
- * 16-byte loads that a wave issues as 1 KiB of one row. A workgroup of 4
- * waves owns 4 * kRows consecutive rows; x is staged into LDS in column
- * chunks once per workgroup and reused by all its rows. Each lane converts
- * its 16 weight bytes to f32 once per row (one v_cvt per byte) and applies
- * them to every batch row of x, so the convert cost is shared across the
- * batch. A wave reduces its 64 partial sums per (row, batch) with
- * cross-lane shuffles and lane 0 applies the scale.
+ * The weights are the traffic: every byte of W is read once, with 16-byte
+ * non-temporal loads, in an order that sweeps W front to back across the
+ * grid. The int8 weights become bf16 pairs exactly (|w| <= 127 fits bf16's
+ * mantissa: a byte-to-f32 convert, then the high halves of two floats) and
+ * meet x in v_dot2_f32_bf16, whose products are exact; every batch row
+ * reuses one conversion.
  */
 #include "../vx_hip_common.h"
 #include "../vx_ops_kernels.h"
+
+#include <algorithm>
 
 namespace vxk {
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 2048; /* columns of x per LDS stage */
+constexpr int kWaves = kThreads / 64;
+constexpr int kGroupCols = kThreads * 16; /* columns one pass of a WG covers */
+constexpr int kMaxRows = 64;              /* rows per workgroup, at most */
+constexpr int kMaxGrid = 2048;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    v += __shfl_xor(v, off, 64);
-  }
-  return v;
-}
-
-__device__ __forceinline__ void bytes_to_f32(u32x4 w, float out[16]) {
+/* int8 bytes of `w` as 8 bf16 pairs (exact). */
+__device__ __forceinline__ void bytes_to_bf16x2(u32x4 w, uint32_t out[8]) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      out[q * 4 + j] = (float)(int8_t)(w[q] >> (8 * j));
-    }
+    const float f0 = (float)(int8_t)(w[q]);
+    const float f1 = (float)(int8_t)(w[q] >> 8);
+    const float f2 = (float)(int8_t)(w[q] >> 16);
+    const float f3 = (float)(int8_t)(w[q] >> 24);
+    out[2 * q] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0),
+                                       0x07060302u);
+    out[2 * q + 1] = __builtin_amdgcn_perm(__float_as_uint(f3),
+                                           __float_as_uint(f2), 0x07060302u);
   }
 }
 
-__device__ __forceinline__ void bf16x16_to_f32(u32x4 lo, u32x4 hi,
-                                               float out[16]) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    out[2 * q] = __uint_as_float(lo[q] << 16);
-    out[2 * q + 1] = __uint_as_float(lo[q] & 0xffff0000u);
-    out[8 + 2 * q] = __uint_as_float(hi[q] << 16);
-    out[8 + 2 * q + 1] = __uint_as_float(hi[q] & 0xffff0000u);
-  }
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                         __builtin_bit_cast(bf16x2, x), acc,
+                                         false);
 }
 
-template <int kB, int kRows>
-__global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
-    const int8_t *__restrict__ W, const float *__restrict__ scale,
-    const uint16_t *__restrict__ X, float *__restrict__ Y, int rows,
-    int cols) {
-  __shared__ u32x4 xs[kB * kChunk / 8];
-  const int t = threadIdx.x;
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int row0 = (blockIdx.x * 4 + wave) * kRows;
+constexpr int log2i(int n) { return n <= 1 ? 0 : 1 + log2i(n / 2); }
 
-  float acc[kRows][kB];
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      acc[r][b] = 0.0f;
-    }
-  }
+/* Lane exchange across the wave with VALU data movement (no LDS
+ * crossbar): the two 32-lane halves and the 16-lane rows trade through
+ * v_permlane32_swap / v_permlane16_swap, lanes within a row through DPP. */
+__device__ __forceinline__ void swap32(float &x, float &y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
+                                                  __float_as_uint(y), false,
+                                                  false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
 
-  for (int c0 = 0; c0 < cols; c0 += kChunk) {
-    const int kc = min(kChunk, cols - c0);
-    const int vecs = kc / 8;
-    for (int i = t; i < kB * vecs; i += kThreads) {
-      const int b = i / vecs;
-      const int v = i - b * vecs;
-      xs[b * (kChunk / 8) + v] = *reinterpret_cast<const u32x4 *>(
-          X + (int64_t)b * cols + c0 + v * 8);
-    }
-    __syncthreads();
-    for (int cc = lane * 16; cc < kc; cc += 64 * 16) {
-      u32x4 wv[kRows];
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) {
-        const int row = row0 + r;
-        wv[r] = row < rows ? __builtin_nontemporal_load(
-                                 reinterpret_cast<const u32x4 *>(
-                                     W + (int64_t)row * cols + c0 + cc))
-                           : u32x4{0, 0, 0, 0};
-      }
-      float wf[kRows][16];
-#pragma unroll
-      for (int r = 0; r < kRows; ++r) {
-        bytes_to_f32(wv[r], wf[r]);
-      }
-#pragma unroll
-      for (int b = 0; b < kB; ++b) {
-        float xf[16];
-        bf16x16_to_f32(xs[b * (kChunk / 8) + cc / 8],
-                       xs[b * (kChunk / 8) + cc / 8 + 1], xf);
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            acc[r][b] += wf[r][j] * xf[j];
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
+__device__ __forceinline__ void swap16(float &x, float &y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x),
+                                                  __float_as_uint(y), false,
+                                                  false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
 
+/* DPP controls pairing lane i of a 16-lane row with the lane differing in
+ * bit 3 (rotate by 8), bit 2 (mirror within 8: i <-> 7-i), bit 1 and bit 0
+ * (quad permutes). */
+template <int kO> constexpr int dpp_partner() {
+  return kO == 8 ? 0x128 : kO == 4 ? 0x141 : kO == 2 ? 0x4e : 0xb1;
+}
+
+template <int kO> __device__ __forceinline__ float from_partner(float v) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(
+      0u, __float_as_uint(v), dpp_partner<kO>(), 0xf, 0xf, false));
+}
+
+/* Sum v[b] over the 64 lanes for every b, as a reduce-scatter: at each of
+ * the first log2(kB) exchange steps (partners across 32, 16, 8, 4, 2, 1
+ * lanes) a lane keeps the sums of half of its values and hands the other
+ * half to its partner; the remaining steps are plain sums. Returns the
+ * batch index whose total this lane holds in v[0]; lanes whose low
+ * 6 - log2(kB) bits are zero are the ones to read. */
+template <int kB, int kStep>
+__device__ __forceinline__ void rs_step(float (&v)[kB], int lane, int &b) {
+  constexpr int kP = log2i(kB);
+  constexpr int kO = 32 >> kStep;
+  if constexpr (kStep < kP) {
+    constexpr int kHalf = kB >> (kStep + 1);
+    const bool up = (lane & kO) != 0;
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const int row = row0 + r;
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const float s = wave_sum(acc[r][b]);
-      if (lane == 0 && row < rows) {
-        Y[(int64_t)b * rows + row] = scale[row] * s;
+    for (int i = 0; i < kHalf; ++i) {
+      if constexpr (kO >= 16) {
+        float x = v[i], y = v[i + kHalf];
+        kO == 32 ? swap32(x, y) : swap16(x, y);
+        v[i] = x + y;
+      } else {
+        const float lo = v[i] + from_partner<kO>(v[i]);
+        const float hi = v[i + kHalf] + from_partner<kO>(v[i + kHalf]);
+        v[i] = up ? hi : lo;
       }
+    }
+    b += up ? kHalf : 0;
+  } else {
+    if constexpr (kO >= 16) {
+      float x = v[0], y = v[0];
+      kO == 32 ? swap32(x, y) : swap16(x, y);
+      v[0] = x + y;
+    } else {
+      v[0] += from_partner<kO>(v[0]);
     }
   }
 }
 
 template <int kB>
+__device__ __forceinline__ int wave_reduce_scatter(float (&v)[kB], int lane) {
+  int b = 0;
+  rs_step<kB, 0>(v, lane, b);
+  rs_step<kB, 1>(v, lane, b);
+  rs_step<kB, 2>(v, lane, b);
+  rs_step<kB, 3>(v, lane, b);
+  rs_step<kB, 4>(v, lane, b);
+  rs_step<kB, 5>(v, lane, b);
+  return b;
+}
+
+/* y[b, r] for kB batch rows (nb of them real, the rest padding), kU
+ * weight rows in flight per pass.
+ *
+ * Workgroup g owns rows g, g + G, g + 2G, ... (G = gridDim.x), so at any
+ * moment the whole grid reads a contiguous band of W. Thread t owns columns
+ * t*16 + j*4096 of every row; for each such column group j it holds its 16
+ * columns of x for every batch row in registers and sweeps its rows, kU at
+ * a time, with 16-byte non-temporal loads (1 KiB per wave instruction, 4 KiB
+ * per row per workgroup). A row's partial sums go through the wave
+ * reduce-scatter and land in LDS, one slot per (row, batch, wave), summed
+ * over the column groups; the 4 waves' slots are added once at the end. */
+template <int kB, int kU>
+__global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
+    const int8_t *__restrict__ W, const float *__restrict__ scale,
+    const uint16_t *__restrict__ X, float *__restrict__ Y, int rows, int cols,
+    int nb) {
+  __shared__ float red[kMaxRows][kB][kWaves];
+  constexpr int kP = log2i(kB);
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int grid = gridDim.x;
+  const int nk = (rows - (int)blockIdx.x + grid - 1) / grid; /* my rows */
+  const bool writer = (lane & ((64 >> kP) - 1)) == 0;
+
+  for (int c0 = 0; c0 < cols; c0 += kGroupCols) {
+    const int c = c0 + t * 16;
+    const bool live = c < cols;
+    u32x4 xl[kB], xh[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const bool ok = live && b < nb;
+      const uint16_t *xp = X + (int64_t)b * cols + c;
+      xl[b] = ok ? *reinterpret_cast<const u32x4 *>(xp) : u32x4{0, 0, 0, 0};
+      xh[b] = ok ? *reinterpret_cast<const u32x4 *>(xp + 8) : u32x4{0, 0, 0, 0};
+    }
+    for (int k0 = 0; k0 < nk; k0 += kU) {
+      u32x4 wv[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int r = (int)blockIdx.x + (k0 + u) * grid;
+        wv[u] = (live && k0 + u < nk)
+                    ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(
+                          W + (int64_t)r * cols + c))
+                    : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        uint32_t wp[8];
+        bytes_to_bf16x2(wv[u], wp);
+        float v[kB];
+#pragma unroll
+        for (int b = 0; b < kB; ++b) {
+          float a = 0.0f;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            a = dot2(wp[p], xl[b][p], a);
+          }
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            a = dot2(wp[4 + p], xh[b][p], a);
+          }
+          v[b] = a;
+        }
+        const int b = wave_reduce_scatter<kB>(v, lane);
+        if (writer && k0 + u < nk) {
+          float &slot = red[k0 + u][b][wave];
+          slot = c0 == 0 ? v[0] : slot + v[0];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < nk * nb; i += kThreads) {
+    const int k = i / nb;
+    const int b = i % nb;
+    const int r = (int)blockIdx.x + k * grid;
+    float v = red[k][b][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+      v += red[k][b][w];
+    }
+    Y[(int64_t)b * rows + r] = scale[r] * v;
+  }
+}
+
+template <int kB>
 void launch_b(const int8_t *w, const float *s, const uint16_t *x, float *y,
-              int rows, int cols, hipStream_t stream) {
-  constexpr int kRows = kB <= 4 ? 2 : 4;
-  const int groups = (rows + 4 * kRows - 1) / (4 * kRows);
-  hipLaunchKernelGGL((gemv_i8_kernel<kB, kRows>), dim3(groups), dim3(kThreads),
-                     0, stream, w, s, x, y, rows, cols);
+              int rows, int cols, int nb, hipStream_t stream) {
+  constexpr int kU = kB <= 4 ? 4 : 2;
+  /* A workgroup loads its slice of x once per column group and reuses it for
+   * all of its rows, so bigger batches take more rows per workgroup (x
+   * traffic 2*kB/rows times the weights) at the cost of fewer workgroups;
+   * never more than kMaxRows rows per workgroup. */
+  constexpr int kTarget = kB <= 2 ? 4 : kB <= 4 ? 8 : 16;
+  int grid = std::min(kMaxGrid, (rows + kTarget - 1) / kTarget);
+  grid = std::max(grid, (rows + kMaxRows - 1) / kMaxRows);
+  hipLaunchKernelGGL((gemv_i8_kernel<kB, kU>), dim3(grid), dim3(kThreads), 0,
+                     stream, w, s, x, y, rows, cols, nb);
 }
 
 } // namespace
@@ -148,31 +243,17 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
       (reinterpret_cast<uintptr_t>(x) & 15)) {
     return false;
   }
-  const int r = (int)rows, c = (int)cols;
-  switch (batch) {
-#define VX_GEMV_CASE(n)                                                        \
-  case n:                                                                      \
-    launch_b<n>(w, scale, x, y, r, c, stream);                                 \
-    break;
-    VX_GEMV_CASE(1)
-    VX_GEMV_CASE(2)
-    VX_GEMV_CASE(3)
-    VX_GEMV_CASE(4)
-    VX_GEMV_CASE(5)
-    VX_GEMV_CASE(6)
-    VX_GEMV_CASE(7)
-    VX_GEMV_CASE(8)
-    VX_GEMV_CASE(9)
-    VX_GEMV_CASE(10)
-    VX_GEMV_CASE(11)
-    VX_GEMV_CASE(12)
-    VX_GEMV_CASE(13)
-    VX_GEMV_CASE(14)
-    VX_GEMV_CASE(15)
-    VX_GEMV_CASE(16)
-#undef VX_GEMV_CASE
-  default:
-    return false;
+  const int r = (int)rows, c = (int)cols, nb = (int)batch;
+  if (nb == 1) {
+    launch_b<1>(w, scale, x, y, r, c, nb, stream);
+  } else if (nb == 2) {
+    launch_b<2>(w, scale, x, y, r, c, nb, stream);
+  } else if (nb <= 4) {
+    launch_b<4>(w, scale, x, y, r, c, nb, stream);
+  } else if (nb <= 8) {
+    launch_b<8>(w, scale, x, y, r, c, nb, stream);
+  } else {
+    launch_b<16>(w, scale, x, y, r, c, nb, stream);
   }
   VX_HIP_CHECK(hipGetLastError());
   return true;
