@@ -34,6 +34,7 @@
 #include "../vx_ops_kernels.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace vxk {
 namespace {
@@ -42,6 +43,11 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#define VX_LDS __attribute__((address_space(3)))
 
 constexpr int kThreads = 256;
 constexpr int kBlockQ = 128;
@@ -63,8 +69,70 @@ __device__ __forceinline__ int swz(int row, int c) {
   }
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+/* K/V planes in LDS keep global order, [key][d] in 16-byte chunks.
+ * K: chunk XORed with the key's low bits so a ds_read_b128 of 16
+ * consecutive keys at one chunk hits distinct banks. V: chunk XORed with a
+ * function of key mod 4, so the transposing read (4 consecutive keys x 32
+ * bytes per 16-lane group) hits distinct banks. */
+template <int kChunks>
+__device__ __forceinline__ int swz_v(int key, int c) {
+  const int q = key & 3;
+  if constexpr (kChunks >= 16) {
+    return c ^ ((q << 1) ^ (q << 2));
+  } else {
+    return c ^ (q << 1);
+  }
+}
+
+/* Buffer descriptor for raw 32-bit-dword loads of `bytes` bytes at `base`;
+ * loads past the end return zeros. */
+__device__ __forceinline__ i32x4 buffer_rsrc(const void *base, int bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+/* One 16-byte-per-lane load straight into LDS (lane i writes lds + 16*i).
+ * Assembly, so the compiler neither waits for it at every LDS read nor
+ * orders it with a fenced barrier; the kernel waits with vmcnt itself. */
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm" /* m0 is reserved: declared */
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ void wait_all_loads() {
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); /* vmcnt(0) */
+}
+
+/* Barrier without the release fence (which would wait for the prefetch);
+ * LDS reads are drained first so a slot is never refilled under a reader. */
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0) */
+  asm volatile("s_barrier" ::: "memory");
+}
+
+/* x of lanes l and l ^ 32 side by side: returns the partner's value. */
+__device__ __forceinline__ float other_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
+                                                  __float_as_uint(x), false,
+                                                  false);
+  /* Lane l < 32 finds lane l + 32's x in r[1]; lane l >= 32 finds lane
+   * l - 32's in r[0]. */
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 template <int kD>
@@ -73,15 +141,17 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O,
     float *__restrict__ LSE, int heads, int group, int seq_q, int seq_k,
     int bh_total, int q_blocks, float scale_log2, bool causal) {
-  constexpr int kKChunks = kD / 8;      /* 16-byte chunks per K row */
-  constexpr int kVChunks = kBlockK / 8; /* 16-byte chunks per V^T row */
-  constexpr int kDSteps = kD / 16;      /* MFMA k-steps over d */
-  constexpr int kDTiles = kD / 32;      /* 32-wide d tiles of O^T */
-  __shared__ u32x4 k_lds[2][kBlockK * kKChunks];
-  __shared__ u32x4 v_lds[2][kD * kVChunks];
+  constexpr int kChunks = kD / 8;                 /* 16-byte chunks per row */
+  constexpr int kUnits = kBlockK * kChunks;       /* 16-byte units per plane */
+  constexpr int kLoads = kUnits / kThreads;       /* per thread per plane */
+  constexpr int kDSteps = kD / 16;                /* MFMA k-steps over d */
+  constexpr int kDTiles = kD / 32;                /* 32-wide d tiles of O^T */
+  constexpr int kRowBytes = kD * 2;
+  /* [stage][K|V][unit] */
+  __shared__ u32x4 ring[2][2][kUnits];
 
   const int t = threadIdx.x;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63;
   const int lq = lane & 31;
   const int g = lane >> 5;
@@ -135,73 +205,43 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
     }
   }
 
-  /* K stage: kBlockK rows x kKChunks chunks, thread-strided. */
-  constexpr int kKLoads = kBlockK * kKChunks / kThreads;
-  /* V stage: thread owns 8 keys (one physical group kg) x 4 d. */
-  const int kg = t & 7;
-  const int dg = t >> 3; /* 0..31: d = 4*dg .. +3; D = 64 uses dg < 16 */
-  constexpr int kVOwners = kD / 4 * 8; /* threads with a V block */
-  int vkey[8];
+  /* Load offsets: unit u = (p * kThreads + t) of a plane is key u / kChunks,
+   * physical chunk u % kChunks, filled from the logical chunk the swizzle
+   * puts there. */
+  uint32_t k_off[kLoads], v_off[kLoads];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    vkey[e] = 16 * (kg >> 1) + 8 * (e >> 2) + 4 * (kg & 1) + (e & 3);
+  for (int p = 0; p < kLoads; ++p) {
+    const int u = p * kThreads + t;
+    const int key = u / kChunks;
+    const int pc = u % kChunks;
+    k_off[p] = (uint32_t)(key * kRowBytes + swz<kChunks>(key, pc) * 16);
+    v_off[p] = (uint32_t)(key * kRowBytes + swz_v<kChunks>(key, pc) * 16);
   }
-
-  u32x4 kreg[kKLoads];
-  u32x2 vreg[8];
-
-  auto fetch = [&](int blk) {
+  const uint32_t ring_base =
+      (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
+  auto issue = [&](int blk) {
     const int key0 = blk * kBlockK;
+    const int bytes = min(kBlockK, seq_k - key0) * kRowBytes;
+    const i32x4 rk = buffer_rsrc(K + kv_base + (int64_t)key0 * kD, bytes);
+    const i32x4 rv = buffer_rsrc(V + kv_base + (int64_t)key0 * kD, bytes);
+    const uint32_t base = ring_base + (uint32_t)((blk & 1) * 2 * kUnits * 16);
 #pragma unroll
-    for (int i = 0; i < kKLoads; ++i) {
-      const int idx = t + i * kThreads;
-      const int row = idx / kKChunks;
-      const int c = idx - row * kKChunks;
-      const int key = key0 + row;
-      kreg[i] = key < seq_k ? *reinterpret_cast<const u32x4 *>(
-                                  K + kv_base + (int64_t)key * kD + c * 8)
-                            : u32x4{0, 0, 0, 0};
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(rk, k_off[p], base + (uint32_t)(p * kThreads + wave * 64) * 16);
     }
-    if (t < kVOwners) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = key0 + vkey[e];
-        vreg[e] = key < seq_k ? *reinterpret_cast<const u32x2 *>(
-                                    V + kv_base + (int64_t)key * kD + 4 * dg)
-                              : u32x2{0, 0};
-      }
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(rv, v_off[p],
+            base + (uint32_t)(kUnits + p * kThreads + wave * 64) * 16);
     }
   };
 
-  auto stash = [&](int s) {
-    u32x4 *kl = k_lds[s];
-#pragma unroll
-    for (int i = 0; i < kKLoads; ++i) {
-      const int idx = t + i * kThreads;
-      const int row = idx / kKChunks;
-      const int c = idx - row * kKChunks;
-      kl[row * kKChunks + swz<kKChunks>(row, c)] = kreg[i];
-    }
-    if (t < kVOwners) {
-      /* 8 keys x 4 d -> 4 rows of V^T, each one 16-byte chunk of 8 keys. */
-      u32x4 *vl = v_lds[s];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int w = j >> 1;
-        const bool hi = j & 1;
-        u32x4 col;
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const uint32_t x = vreg[2 * qd][w];
-          const uint32_t y = vreg[2 * qd + 1][w];
-          col[qd] = hi ? ((x >> 16) | (y & 0xffff0000u))
-                       : ((x & 0xffffu) | (y << 16));
-        }
-        const int row = 4 * dg + j;
-        vl[row * kVChunks + swz<kVChunks>(row, kg)] = col;
-      }
-    }
-  };
+  /* Transposed V read: lane (g, row group j = (lane >> 4) & 1, i = lane &
+   * 15) reads key 4g + 8h + i/4 of a 16-key step at d 16j + 4(i%4) of a
+   * 32-wide d tile, which hands each lane the 8 keys its MFMA k-slots need
+   * (the P^T order below) at d = lane % 32. */
+  const int tr_key = 4 * g + ((lane & 15) >> 2);
+  const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   f32x16 o_acc[kDTiles];
 #pragma unroll
@@ -213,61 +253,79 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
   }
   float m_run = -INFINITY; /* base-2 running max of this lane's query */
   float l_run = 0.0f;
+  const bool scale_pos = scale_log2 >= 0.0f;
 
   if (nblocks > 0) {
-    fetch(0);
-    stash(0);
+    issue(0);
   }
-  __syncthreads();
   for (int blk = 0; blk < nblocks; ++blk) {
-    const int s = blk & 1;
+    wait_all_loads();
+    lds_barrier();
     if (blk + 1 < nblocks) {
-      fetch(blk + 1);
+      issue(blk + 1);
     }
     const int key0 = blk * kBlockK;
-    if (key0 <= wave_last) {
-      const u32x4 *kl = k_lds[s];
-      const u32x4 *vl = v_lds[s];
-      /* S^T for keys key0 + 32*kt + (row), queries qw0 + lq. */
-      f32x16 st[2];
+    if (key0 > wave_last) {
+      continue;
+    }
+    const u32x4 *kl = ring[blk & 1][0];
+    const VX_LDS char *vl = (const VX_LDS char *)&ring[blk & 1][1][0];
+
+    /* S^T for keys key0 + 32*kt + (row), queries qw0 + lq. */
+    f32x16 st[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        st[kt][r] = 0.0f;
+      }
+      const int row = kt * 32 + lq;
+#pragma unroll
+      for (int ds = 0; ds < kDSteps; ++ds) {
+        const u32x4 a = kl[row * kChunks + swz<kChunks>(row, 2 * ds + g)];
+        st[kt] = mfma(a, qf[ds], st[kt]);
+      }
+    }
+
+    /* Row max in raw scores (the scale's sign picks max or min), masked
+     * keys excluded. */
+    const bool need_mask =
+        key0 + kBlockK > seq_k || (causal && key0 + kBlockK - 1 > qw0 + shift);
+    const int limit = causal ? min(seq_k - 1, my_q + shift) : seq_k - 1;
+    const float hide = scale_pos ? -INFINITY : INFINITY;
+    if (need_mask) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          st[kt][r] = 0.0f;
-        }
-        const int row = kt * 32 + lq;
-#pragma unroll
-        for (int ds = 0; ds < kDSteps; ++ds) {
-          const u32x4 a = kl[row * kKChunks + swz<kKChunks>(row, 2 * ds + g)];
-          st[kt] = mfma(a, qf[ds], st[kt]);
+          const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+          st[kt][r] = key <= limit ? st[kt][r] : hide;
         }
       }
-      /* Scale into base 2 and mask keys past the diagonal or the sequence. */
-      const bool need_mask =
-          key0 + kBlockK > seq_k || (causal && key0 + kBlockK - 1 > qw0 + shift);
-      const int limit = causal ? min(seq_k - 1, my_q + shift) : seq_k - 1;
-      float mx = -INFINITY;
+    }
+    float ext = hide;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = st[kt][r] * scale_log2;
-          if (need_mask) {
-            const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
-            x = key <= limit ? x : -INFINITY;
-          }
-          st[kt][r] = x;
-          mx = fmaxf(mx, x);
-        }
+      for (int r = 0; r < 16; ++r) {
+        ext = scale_pos ? fmaxf(ext, st[kt][r]) : fminf(ext, st[kt][r]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run, mx);
-      /* All keys so far masked: keep exponents finite (everything is 0). */
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      float psum = 0.0f;
-      u32x4 pt[4]; /* P^T operands for the 4 key steps of 16 */
+    }
+    {
+      const float o = other_half(ext);
+      ext = scale_pos ? fmaxf(ext, o) : fminf(ext, o);
+    }
+    const float mx = ext == hide ? -INFINITY : ext * scale_log2;
+    const float m_new = fmaxf(m_run, mx);
+    /* All keys so far masked: keep exponents finite (everything is 0). */
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+
+    /* P = 2^(s * scale - m); masked scores (+-inf in raw form) are set to
+     * exactly 0. */
+    float psum = 0.0f;
+    u32x4 pt[4]; /* P^T operands for the 4 key steps of 16 */
+    auto probs = [&](auto masked) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -275,20 +333,30 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
           float p[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            p[e] = exp2f(st[kt][8 * hh + e] - m_use);
+            const float x = st[kt][8 * hh + e];
+            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, -m_use));
+            if constexpr (decltype(masked)::value) {
+              p[e] = x == hide ? 0.0f : p[e];
+            }
             psum += p[e];
           }
-          u32x4 v;
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
-            v[w] = pack_bf16(p[2 * w], p[2 * w + 1]);
+            pt[2 * kt + hh][w] = pack2(p[2 * w], p[2 * w + 1]);
           }
-          pt[2 * kt + hh] = v;
         }
       }
-      psum += __shfl_xor(psum, 32, 64);
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
+    };
+    if (need_mask) {
+      probs(std::true_type{});
+    } else {
+      probs(std::false_type{});
+    }
+    psum += other_half(psum);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    /* Rescale O only when some lane's max moved (alpha < 1). */
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
       for (int i = 0; i < kDTiles; ++i) {
 #pragma unroll
@@ -296,21 +364,29 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
           o_acc[i][r] *= alpha;
         }
       }
-      /* O^T += V^T P^T over the 4 key steps. */
+    }
+
+    /* O^T += V^T P^T over the 4 key steps. */
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-        for (int i = 0; i < kDTiles; ++i) {
-          const int row = i * 32 + lq;
-          const u32x4 a = vl[row * kVChunks + swz<kVChunks>(row, 2 * ks + g)];
-          o_acc[i] = mfma(a, pt[ks], o_acc[i]);
+      for (int i = 0; i < kDTiles; ++i) {
+        const int d = 32 * i + tr_d;
+        u32x4 a;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int key = 16 * ks + tr_key + 8 * hh;
+          const int at = key * kRowBytes + swz_v<kChunks>(key, d >> 3) * 16 +
+                         (d & 7) * 2;
+          const u32x2 w = __builtin_bit_cast(
+              u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                         (VX_LDS i16x4 *)(vl + at)));
+          a[2 * hh] = w[0];
+          a[2 * hh + 1] = w[1];
         }
+        o_acc[i] = mfma(a, pt[ks], o_acc[i]);
       }
     }
-    if (blk + 1 < nblocks) {
-      stash(s ^ 1);
-    }
-    __syncthreads();
   }
 
   if (my_q >= seq_q) {
@@ -324,8 +400,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
     for (int r4 = 0; r4 < 4; ++r4) {
       const int d = i * 32 + 8 * r4 + 4 * g;
       u32x2 out;
-      out[0] = pack_bf16(o_acc[i][4 * r4] * inv, o_acc[i][4 * r4 + 1] * inv);
-      out[1] = pack_bf16(o_acc[i][4 * r4 + 2] * inv, o_acc[i][4 * r4 + 3] * inv);
+      out[0] = pack2(o_acc[i][4 * r4] * inv, o_acc[i][4 * r4 + 1] * inv);
+      out[1] = pack2(o_acc[i][4 * r4 + 2] * inv, o_acc[i][4 * r4 + 3] * inv);
       *reinterpret_cast<u32x2 *>(orow + d) = out;
     }
   }
