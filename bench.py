@@ -55,6 +55,25 @@ def traffic_from_profiles(name: str):
     return None
 
 
+SETTLE_MS = 200.0  # untimed GPU work before each kernel's warmup steps
+
+
+def settle(call, timer, min_ms: float = SETTLE_MS) -> float:
+    """Run `call` untimed until at least `min_ms` of GPU time has passed, so
+    the timed steps see the clocks a sustained workload runs at (a cold GPU
+    measures up to a quarter slower on the first milliseconds). Returns the
+    GPU milliseconds spent."""
+    spent = 0.0
+    while spent < min_ms:
+        e0, e1 = timer.event(), timer.event()
+        timer.record(e0)
+        for _ in range(10):
+            call()
+        timer.record(e1)
+        spent += timer.elapsed_ms(e0, e1)
+    return spent
+
+
 def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     from vx_amd import abi
     from vx_amd.abi import f32_to_bf16
@@ -76,6 +95,13 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     dispatch = lib.lib.vx_plugin_dispatch_async
 
     before = lib.stats()
+    settled = [0]
+
+    def one():
+        dispatch(buf, len(pl), argv, tags, nargs)
+        settled[0] += 1
+
+    settle(one, timer)
     for _ in range(warmup):
         dispatch(buf, len(pl), argv, tags, nargs)
     timer.sync()
@@ -89,7 +115,8 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     timer.sync()
     wall = time.perf_counter() - t0
     after = lib.stats()
-    assert after["gemm_mfma"] - before["gemm_mfma"] == steps + warmup, "GEMM did not take the MFMA path"
+    assert after["gemm_mfma"] - before["gemm_mfma"] == steps + warmup + settled[0], \
+        "GEMM did not take the MFMA path"
     c = dc.numpy()
     assert np.isfinite(c).all()
     for x in (da, db, dc):
@@ -117,6 +144,7 @@ def bench_fa(lib, timer, steps: int, warmup: int):
         rc = flash_attention_fwd(lib, q, k, v, do.ptr, dl.ptr, b, h, h, s, s, d, 1.0 / np.sqrt(d), True)
         assert rc == 0
 
+    settle(call, timer)
     for _ in range(warmup):
         call()
     timer.sync()
@@ -244,7 +272,7 @@ def main() -> int:
     extra = {}
     if "fa" in only:
         log("flash attention config 3")
-        extra["flash_attn_fwd"] = bench_fa(lib, timer, max(5, ns.steps // 5), 2)
+        extra["flash_attn_fwd"] = bench_fa(lib, timer, max(10, ns.steps // 2), 3)
         log(f"fa {extra['flash_attn_fwd']['tflops']:.1f} TFLOP/s")
     if "gemv" in only:
         log("int8 gemv config 5")
@@ -274,6 +302,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": ns.steps,
         "warmup": ns.warmup,
+        "settle_ms": SETTLE_MS,
         "ms_per_step": round(g["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",

@@ -2,33 +2,35 @@
  * flash_attn.hip -- flash-attention forward on gfx950 MFMA (bf16 in, f32
  * accumulate, bf16 out, f32 log-sum-exp).
  *
- * Workgroup = 4 waves = 128 query rows of one (batch, head); each wave owns
- * 32 rows. K and V walk in blocks of 64 keys through a double-buffered LDS
- * ring, one barrier per block.
+ * Workgroup = 4 waves; each wave owns 32 * kQT query rows of one
+ * (batch, head) (kQT = 1 by default: two workgroups share a CU, so one
+ * wave's softmax runs beside the other's MFMAs). K and V walk in blocks of
+ * kBK keys through a two-slot LDS ring filled by buffer-to-LDS loads, in
+ * their global [key][d] order; one barrier per block.
  *
- * The wave computes the transposed products so the softmax needs no
+ * The wave computes the transposed products so the softmax needs almost no
  * cross-lane data movement:
- *   S^T[key][q] = K Q^T   (v_mfma_f32_32x32x16_bf16; A = K rows from LDS,
- *                          B = Q^T, the wave's Q held in registers)
- *   O^T[d][q]  += V^T P^T (A = V^T from LDS, B = P^T straight from the S^T
- *                          accumulators)
+ *   S^T[key][q] = K Q^T   (v_mfma_f32_32x32x16_bf16; A = K rows read with
+ *                          ds_read_b128, B = Q^T held in registers)
+ *   O^T[d][q]  += V^T P^T (A = V^T read with ds_read_b64_tr_b16 from the
+ *                          [key][d] plane, B = P^T from the S^T accumulators)
  * In the 32x32 accumulator layout lane l holds column l % 32 -- one query --
  * so a query's running max and sum live in lane l and its partner l ^ 32:
- * the row reduction is 16 in-lane steps and one cross-lane exchange. The
- * MFMA's k-slots of lane group g = l / 32 are keys {4g..4g+3, 8+4g..8+4g+3}
- * of each 16-key step, which is exactly the key set the S^T accumulator
- * elements 8h..8h+7 of that lane hold, so P^T is S^T rounded to bf16 in
- * place. V is stored in LDS transposed ([d][key]) with the keys of each
- * 16-key step in that same order, built by an 8x4 register transpose on the
- * way in; its rows are XOR-swizzled in 16-byte chunks for conflict-free
- * ds_read_b128.
+ * the row reduction is in-lane plus one v_permlane32_swap. The MFMA's
+ * k-slots of lane group g = l / 32 are keys {4g..4g+3, 8+4g..8+4g+3} of each
+ * 16-key step, exactly the key set the S^T accumulator elements 8h..8h+7 of
+ * that lane hold, so P^T is S^T converted to bf16 in place; the transposing
+ * V read is addressed to hand each lane those same keys.
  *
- * Softmax runs in base 2 with scale * log2(e) folded into one multiply;
- * lse = (m + log2(l)) * ln 2. A row that sees no key writes o = 0 and
- * lse = -inf. Causal blocks past a wave's last visible key are skipped; the
- * diagonal and the sequence tail are masked. Workgroups start with the
- * heaviest query blocks (causal work grows with the block index) and keep a
- * head's blocks on one XCD when the head count allows.
+ * Softmax runs in base 2: p = 2^(s * scale * log2(e) - m) with the scale
+ * folded into one fma; lse = (m + log2(l)) * ln 2. The reference max m only
+ * moves when a block's max passes it by more than 2^8, so most blocks skip
+ * rescaling O. A row that sees no key writes o = 0 and lse = -inf. Causal
+ * blocks past a wave's last visible key are skipped; the diagonal and the
+ * sequence tail are masked. K is requested two blocks ahead and V one, so
+ * the next block's score MFMAs are issued while this block's softmax runs.
+ * Workgroups start with the heaviest query blocks (causal work grows with
+ * the block index); each XCD keeps a few heads' K/V in its L2 at a time.
  */
 #include "../vx_hip_common.h"
 #include "../vx_ops_kernels.h"
@@ -50,8 +52,28 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #define VX_LDS __attribute__((address_space(3)))
 
 constexpr int kThreads = 256;
-constexpr int kBlockQ = 128;
-constexpr int kBlockK = 64;
+/* Query tiles of 32 per wave (a workgroup of 4 waves covers 128 * kQT
+ * queries) and keys per K/V block (a multiple of 32). Two tiles halve the
+ * LDS operand reads per MFMA but need one wave per SIMD, which loses more
+ * to exposed latency than it saves (measured: 508 vs 820 TFLOP/s for the
+ * causal [4,32,2048,128] case). */
+#ifndef VX_FA_QT
+#define VX_FA_QT 1
+#endif
+#ifndef VX_FA_BK
+#define VX_FA_BK 64
+#endif
+/* VALU instructions the scheduler places after each score MFMA in the
+ * straight-line softmax region (measured best at 3 for head_dim 128). */
+#ifndef VX_FA_SGB
+#define VX_FA_SGB 3
+#endif
+constexpr float kSlack = 8.0f; /* base-2 headroom of the stale row max */
+/* Heads an XCD works through together (0: all of its heads at once). */
+#ifndef VX_FA_HG
+#define VX_FA_HG 4
+#endif
+constexpr int kHeadGroup = VX_FA_HG;
 
 __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
@@ -120,14 +142,13 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-/* x of lanes l and l ^ 32 side by side: returns the partner's value. */
-__device__ __forceinline__ float other_half(float x) {
+/* x of lanes l and l ^ 32: each lane gets both values (its own and its
+ * partner's, in some order), for a max or a sum across the two halves. */
+__device__ __forceinline__ f32x2 halves(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
                                                   __float_as_uint(x), false,
                                                   false);
-  /* Lane l < 32 finds lane l + 32's x in r[1]; lane l >= 32 finds lane
-   * l - 32's in r[0]. */
-  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  return f32x2{__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
@@ -135,18 +156,25 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-template <int kD>
-__global__ __launch_bounds__(kThreads, 2) void flash_fwd(
+/* kQT query tiles of 32 per wave: a wave owns 32 * kQT queries, so each K
+ * and V operand read from LDS feeds kQT MFMAs. */
+template <int kD, int kQT, int kBK>
+__global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O,
     float *__restrict__ LSE, int heads, int group, int seq_q, int seq_k,
     int bh_total, int q_blocks, float scale_log2, bool causal) {
+  constexpr int kBlockK = kBK;                    /* keys per block */
+  constexpr int kKT = kBlockK / 32;               /* 32-key tiles per block */
+  constexpr int kKS = kBlockK / 16;               /* 16-key MFMA steps */
   constexpr int kChunks = kD / 8;                 /* 16-byte chunks per row */
   constexpr int kUnits = kBlockK * kChunks;       /* 16-byte units per plane */
   constexpr int kLoads = kUnits / kThreads;       /* per thread per plane */
   constexpr int kDSteps = kD / 16;                /* MFMA k-steps over d */
   constexpr int kDTiles = kD / 32;                /* 32-wide d tiles of O^T */
   constexpr int kRowBytes = kD * 2;
+  constexpr int kWaveQ = 32 * kQT;                /* queries per wave */
+  constexpr int kBlockQ = 4 * kWaveQ;             /* queries per workgroup */
   /* [stage][K|V][unit] */
   __shared__ u32x4 ring[2][2][kUnits];
 
@@ -156,16 +184,26 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
   const int lq = lane & 31;
   const int g = lane >> 5;
 
-  /* Launch order -> (head, query block): heaviest blocks first, and one
-   * head's blocks on one XCD (workgroup i runs on XCD i % 8). */
+  /* Launch order -> (head, query block). Workgroup i runs on XCD i % 8, so
+   * each XCD gets every 8th head; it walks them kHeadGroup heads at a time
+   * (all query blocks of the group, heaviest first), which keeps the K/V of
+   * only a few heads live in its L2 at once. */
   int id = blockIdx.x;
   int bh, qb;
   if ((bh_total & 7) == 0) {
     const int xcd = id & 7;
     const int local = id >> 3;
     const int per = bh_total >> 3;
-    bh = xcd + 8 * (local % per);
-    qb = q_blocks - 1 - local / per;
+    if (kHeadGroup > 0 && per % kHeadGroup == 0) {
+      const int span = kHeadGroup * q_blocks;
+      const int grp = local / span;
+      const int in = local - grp * span;
+      bh = xcd + 8 * (grp * kHeadGroup + in % kHeadGroup);
+      qb = q_blocks - 1 - in / kHeadGroup;
+    } else {
+      bh = xcd + 8 * (local % per);
+      qb = q_blocks - 1 - local / per;
+    }
   } else {
     bh = id % bh_total;
     qb = q_blocks - 1 - id / bh_total;
@@ -180,28 +218,29 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
   const int shift = seq_k - seq_q; /* query i sees keys <= i + shift */
 
   const int q0 = qb * kBlockQ;
-  const int qw0 = q0 + wave * 32;
-  const int my_q = qw0 + lq;
+  const int qw0 = q0 + wave * kWaveQ;
 
   /* Keys any row of this workgroup may see, and this wave's last key. */
   int kv_end = seq_k;
   int wave_last = seq_k - 1;
   if (causal) {
     kv_end = min(seq_k, q0 + kBlockQ + shift);
-    wave_last = min(seq_k - 1, qw0 + 31 + shift);
+    wave_last = min(seq_k - 1, qw0 + kWaveQ - 1 + shift);
   }
   const int nblocks = kv_end > 0 ? (kv_end + kBlockK - 1) / kBlockK : 0;
 
-  /* The wave's Q^T as MFMA B operands: lane (q = lq, group g) holds
-   * d = 16s + 8g .. +8 for each d-step s. */
-  u32x4 qf[kDSteps];
-  {
-    const bool ok = my_q < seq_q;
-    const uint16_t *src = Q + q_base + (int64_t)(ok ? my_q : 0) * kD + 8 * g;
+  /* The wave's Q^T as MFMA B operands: lane (q = lq, group g) of tile qt
+   * holds d = 16s + 8g .. +8 of query qw0 + 32 qt + lq for each d-step s. */
+  u32x4 qf[kQT][kDSteps];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    const int q = qw0 + 32 * qt + lq;
+    const bool ok = q < seq_q;
+    const uint16_t *src = Q + q_base + (int64_t)(ok ? q : 0) * kD + 8 * g;
 #pragma unroll
     for (int s = 0; s < kDSteps; ++s) {
-      qf[s] = ok ? *reinterpret_cast<const u32x4 *>(src + 16 * s)
-                 : u32x4{0, 0, 0, 0};
+      qf[qt][s] = ok ? *reinterpret_cast<const u32x4 *>(src + 16 * s)
+                     : u32x4{0, 0, 0, 0};
     }
   }
 
@@ -219,20 +258,18 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
   }
   const uint32_t ring_base =
       (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
-  auto issue = [&](int blk) {
+  /* Block b of K and of V lives in slot b % 2 of its plane. */
+  auto issue = [&](int blk, int plane) {
     const int key0 = blk * kBlockK;
     const int bytes = min(kBlockK, seq_k - key0) * kRowBytes;
-    const i32x4 rk = buffer_rsrc(K + kv_base + (int64_t)key0 * kD, bytes);
-    const i32x4 rv = buffer_rsrc(V + kv_base + (int64_t)key0 * kD, bytes);
-    const uint32_t base = ring_base + (uint32_t)((blk & 1) * 2 * kUnits * 16);
+    const uint16_t *src = plane == 0 ? K : V;
+    const i32x4 rs = buffer_rsrc(src + kv_base + (int64_t)key0 * kD, bytes);
+    const uint32_t *off = plane == 0 ? k_off : v_off;
+    const uint32_t base =
+        ring_base + (uint32_t)((((blk & 1) * 2 + plane) * kUnits + wave * 64) * 16);
 #pragma unroll
     for (int p = 0; p < kLoads; ++p) {
-      dma16(rk, k_off[p], base + (uint32_t)(p * kThreads + wave * 64) * 16);
-    }
-#pragma unroll
-    for (int p = 0; p < kLoads; ++p) {
-      dma16(rv, v_off[p],
-            base + (uint32_t)(kUnits + p * kThreads + wave * 64) * 16);
+      dma16(rs, off[p], base + (uint32_t)(p * kThreads * 16));
     }
   };
 
@@ -243,132 +280,126 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
   const int tr_key = 4 * g + ((lane & 15) >> 2);
   const int tr_d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  f32x16 o_acc[kDTiles];
+  f32x16 o_acc[kQT][kDTiles];
 #pragma unroll
-  for (int i = 0; i < kDTiles; ++i) {
+  for (int qt = 0; qt < kQT; ++qt) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      o_acc[i][r] = 0.0f;
-    }
-  }
-  float m_run = -INFINITY; /* base-2 running max of this lane's query */
-  float l_run = 0.0f;
-  const bool scale_pos = scale_log2 >= 0.0f;
-
-  if (nblocks > 0) {
-    issue(0);
-  }
-  for (int blk = 0; blk < nblocks; ++blk) {
-    wait_all_loads();
-    lds_barrier();
-    if (blk + 1 < nblocks) {
-      issue(blk + 1);
-    }
-    const int key0 = blk * kBlockK;
-    if (key0 > wave_last) {
-      continue;
-    }
-    const u32x4 *kl = ring[blk & 1][0];
-    const VX_LDS char *vl = (const VX_LDS char *)&ring[blk & 1][1][0];
-
-    /* S^T for keys key0 + 32*kt + (row), queries qw0 + lq. */
-    f32x16 st[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int i = 0; i < kDTiles; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        st[kt][r] = 0.0f;
-      }
-      const int row = kt * 32 + lq;
-#pragma unroll
-      for (int ds = 0; ds < kDSteps; ++ds) {
-        const u32x4 a = kl[row * kChunks + swz<kChunks>(row, 2 * ds + g)];
-        st[kt] = mfma(a, qf[ds], st[kt]);
+        o_acc[qt][i][r] = 0.0f;
       }
     }
+  }
+  /* Base-2 running reference max and sum of this lane's query per tile. */
+  float m_run[kQT], l_run[kQT];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.0f;
+  }
 
-    /* Row max in raw scores (the scale's sign picks max or min), masked
-     * keys excluded. */
-    const bool need_mask =
-        key0 + kBlockK > seq_k || (causal && key0 + kBlockK - 1 > qw0 + shift);
-    const int limit = causal ? min(seq_k - 1, my_q + shift) : seq_k - 1;
-    const float hide = scale_pos ? -INFINITY : INFINITY;
-    if (need_mask) {
+  typedef f32x16 Scores[kKT][kQT]; /* [key tile][query tile] */
+
+  /* S^T of block `blk` for this wave: keys 32*kt + (row), queries of tile
+   * qt; one K operand read feeds all query tiles. */
+  auto scores = [&](int blk, Scores &st) {
+    const u32x4 *kl = ring[blk & 1][0];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+    for (int ds = 0; ds < kDSteps; ++ds) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
-          st[kt][r] = key <= limit ? st[kt][r] : hide;
+      for (int kt = 0; kt < kKT; ++kt) {
+        const int row = kt * 32 + lq;
+        const u32x4 a = kl[row * kChunks + swz<kChunks>(row, 2 * ds + g)];
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          st[kt][qt] = mfma(a, qf[qt][ds], ds == 0 ? f32x16{} : st[kt][qt]);
         }
       }
     }
-    float ext = hide;
+  };
+
+  const float hide = scale_log2 >= 0.0f ? -INFINITY : INFINITY;
+
+  /* Softmax of one query tile's raw scores against its running reference
+   * max: the P^T operands in `pt`, the factor O and l take, and whether the
+   * reference moved. Masked scores are +-inf (the scale's sign) in raw form
+   * and come out as exactly 0. */
+  auto softmax = [&](Scores &st, int qt, u32x4 (&pt)[kKS], float &alpha,
+                     auto masked, auto pos) -> bool {
+    constexpr bool kMasked = decltype(masked)::value;
+    constexpr bool kPos = decltype(pos)::value;
+    float ext = kPos ? -INFINITY : INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < kKT; ++kt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        ext = scale_pos ? fmaxf(ext, st[kt][r]) : fminf(ext, st[kt][r]);
+        ext = kPos ? fmaxf(ext, st[kt][qt][r]) : fminf(ext, st[kt][qt][r]);
       }
     }
     {
-      const float o = other_half(ext);
-      ext = scale_pos ? fmaxf(ext, o) : fminf(ext, o);
+      const auto r = halves(ext);
+      ext = kPos ? fmaxf(r[0], r[1]) : fminf(r[0], r[1]);
     }
     const float mx = ext == hide ? -INFINITY : ext * scale_log2;
-    const float m_new = fmaxf(m_run, mx);
+    /* The reference max m moves only when a block's max passes it by more
+     * than kSlack (and always from -inf): p = 2^(s - m) then stays below
+     * 2^kSlack, and O and l share the stale m, so the result is the same up
+     * to rounding while most blocks skip the O rescale. */
+    const bool bump = mx > m_run[qt] + kSlack;
+    const float m_next = bump ? mx : m_run[qt];
     /* All keys so far masked: keep exponents finite (everything is 0). */
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-
-    /* P = 2^(s * scale - m); masked scores (+-inf in raw form) are set to
-     * exactly 0. */
+    const float m_use = m_next == -INFINITY ? 0.0f : m_next;
+    alpha = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_use) : 1.0f;
     float psum = 0.0f;
-    u32x4 pt[4]; /* P^T operands for the 4 key steps of 16 */
-    auto probs = [&](auto masked) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < kKT; ++kt) {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float p[8];
+      for (int hh = 0; hh < 2; ++hh) {
+        float p[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = st[kt][8 * hh + e];
-            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, -m_use));
-            if constexpr (decltype(masked)::value) {
-              p[e] = x == hide ? 0.0f : p[e];
-            }
-            psum += p[e];
+        for (int e = 0; e < 8; ++e) {
+          const float x = st[kt][qt][8 * hh + e];
+          p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, -m_use));
+          if constexpr (kMasked) {
+            p[e] = x == hide ? 0.0f : p[e];
           }
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            pt[2 * kt + hh][w] = pack2(p[2 * w], p[2 * w + 1]);
-          }
+          psum += p[e];
         }
-      }
-    };
-    if (need_mask) {
-      probs(std::true_type{});
-    } else {
-      probs(std::false_type{});
-    }
-    psum += other_half(psum);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-    /* Rescale O only when some lane's max moved (alpha < 1). */
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-      for (int i = 0; i < kDTiles; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          o_acc[i][r] *= alpha;
+        for (int w = 0; w < 4; ++w) {
+          pt[2 * kt + hh][w] = pack2(p[2 * w], p[2 * w + 1]);
         }
       }
     }
+    {
+      const auto r = halves(psum);
+      psum = r[0] + r[1];
+    }
+    l_run[qt] = l_run[qt] * alpha + psum;
+    m_run[qt] = m_next;
+    return bump;
+  };
 
-    /* O^T += V^T P^T over the 4 key steps. */
+  /* O^T = alpha O^T + V^T P^T over the 4 key steps of block `blk`; one V
+   * operand read feeds all query tiles. */
+  auto accumulate = [&](int blk, const u32x4 (&pt)[kQT][kKS],
+                        const float (&alpha)[kQT], const bool (&bump)[kQT]) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int qt = 0; qt < kQT; ++qt) {
+      if (__builtin_amdgcn_ballot_w64(bump[qt]) != 0) {
+#pragma unroll
+        for (int i = 0; i < kDTiles; ++i) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            o_acc[qt][i][r] *= alpha[qt];
+          }
+        }
+      }
+    }
+    const VX_LDS char *vl = (const VX_LDS char *)&ring[blk & 1][1][0];
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) {
 #pragma unroll
       for (int i = 0; i < kDTiles; ++i) {
         const int d = 32 * i + tr_d;
@@ -384,32 +415,151 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd(
           a[2 * hh] = w[0];
           a[2 * hh + 1] = w[1];
         }
-        o_acc[i] = mfma(a, pt[ks], o_acc[i]);
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          o_acc[qt][i] = mfma(a, pt[qt][ks], o_acc[qt][i]);
+        }
       }
+    }
+  };
+
+  /* One key block. Entering it, K of this block and the next and V of this
+   * block have been requested, and this block's scores are in `st`. After
+   * the barrier the slots of the previous block are free: K two blocks
+   * ahead and V one block ahead go into them. The next block's score MFMAs
+   * are issued alongside this block's softmax; on a block that needs no
+   * mask (the common case) they form one straight-line region whose MFMAs
+   * are spread between the softmax's VALU instructions. */
+  auto step = [&](int blk, Scores &st, Scores &sn) {
+    wait_all_loads();
+    lds_barrier();
+    if (blk + 2 < nblocks) {
+      issue(blk + 2, 0);
+    }
+    if (blk + 1 < nblocks) {
+      issue(blk + 1, 1);
+    }
+    const int key0 = blk * kBlockK;
+    if (key0 > wave_last) {
+      return;
+    }
+    const bool need_mask =
+        key0 + kBlockK > seq_k || (causal && key0 + kBlockK - 1 > qw0 + shift);
+    const bool next = blk + 1 < nblocks && key0 + kBlockK <= wave_last;
+    u32x4 pt[kQT][kKS];
+    float alpha[kQT];
+    bool bump[kQT];
+    if (!need_mask && next && scale_log2 >= 0.0f) {
+      scores(blk + 1, sn);
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        bump[qt] = softmax(st, qt, pt[qt], alpha[qt], std::false_type{},
+                           std::true_type{});
+      }
+#if VX_FA_SGB > 0
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); /* DS read */
+#pragma unroll
+      for (int i = 0; i < 8 * kKT * kQT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* MFMA */
+        __builtin_amdgcn_sched_group_barrier(0x002, VX_FA_SGB, 0); /* VALU */
+        if (i < 12) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+#endif
+    } else {
+      if (next) {
+        scores(blk + 1, sn);
+      }
+      if (need_mask || scale_log2 < 0.0f) {
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          const int my_q = qw0 + 32 * qt + lq;
+          const int limit =
+              causal ? min(seq_k - 1, my_q + shift) : seq_k - 1;
+#pragma unroll
+          for (int kt = 0; kt < kKT; ++kt) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+              st[kt][qt][r] = key <= limit ? st[kt][qt][r] : hide;
+            }
+          }
+          bump[qt] = scale_log2 >= 0.0f
+                         ? softmax(st, qt, pt[qt], alpha[qt], std::true_type{},
+                                   std::true_type{})
+                         : softmax(st, qt, pt[qt], alpha[qt], std::true_type{},
+                                   std::false_type{});
+        }
+      } else {
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          bump[qt] = softmax(st, qt, pt[qt], alpha[qt], std::false_type{},
+                             std::true_type{});
+        }
+      }
+    }
+    accumulate(blk, pt, alpha, bump);
+  };
+
+  Scores sa, sb;
+  if (nblocks > 0) {
+    issue(0, 0);
+    issue(0, 1);
+    if (nblocks > 1) {
+      issue(1, 0);
+    }
+    wait_all_loads();
+    lds_barrier();
+    if (0 <= wave_last) {
+      scores(0, sa);
+    }
+  }
+  for (int blk = 0; blk < nblocks; blk += 2) {
+    step(blk, sa, sb);
+    if (blk + 1 < nblocks) {
+      step(blk + 1, sb, sa);
     }
   }
 
-  if (my_q >= seq_q) {
-    return;
-  }
-  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  uint16_t *orow = O + q_base + (int64_t)my_q * kD;
 #pragma unroll
-  for (int i = 0; i < kDTiles; ++i) {
+  for (int qt = 0; qt < kQT; ++qt) {
+    const int my_q = qw0 + 32 * qt + lq;
+    if (my_q >= seq_q) {
+      continue;
+    }
+    const float inv = l_run[qt] > 0.0f ? 1.0f / l_run[qt] : 0.0f;
+    uint16_t *orow = O + q_base + (int64_t)my_q * kD;
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int d = i * 32 + 8 * r4 + 4 * g;
-      u32x2 out;
-      out[0] = pack2(o_acc[i][4 * r4] * inv, o_acc[i][4 * r4 + 1] * inv);
-      out[1] = pack2(o_acc[i][4 * r4 + 2] * inv, o_acc[i][4 * r4 + 3] * inv);
-      *reinterpret_cast<u32x2 *>(orow + d) = out;
+    for (int i = 0; i < kDTiles; ++i) {
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int d = i * 32 + 8 * r4 + 4 * g;
+        u32x2 out;
+        out[0] = pack2(o_acc[qt][i][4 * r4] * inv, o_acc[qt][i][4 * r4 + 1] * inv);
+        out[1] = pack2(o_acc[qt][i][4 * r4 + 2] * inv,
+                       o_acc[qt][i][4 * r4 + 3] * inv);
+        *reinterpret_cast<u32x2 *>(orow + d) = out;
+      }
+    }
+    if (LSE && g == 0) {
+      LSE[(int64_t)bh * seq_q + my_q] =
+          l_run[qt] > 0.0f
+              ? (m_run[qt] + log2f(l_run[qt])) * 0.69314718055994531f
+              : -INFINITY;
     }
   }
-  if (LSE && g == 0) {
-    LSE[(int64_t)bh * seq_q + my_q] =
-        l_run > 0.0f ? (m_run + log2f(l_run)) * 0.69314718055994531f
-                     : -INFINITY;
-  }
+}
+
+template <int kD, int kQT, int kBK>
+void launch(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+            uint16_t *o, float *lse, int heads, int group, int seq_q, int seq_k,
+            int bh, float scale_log2, bool causal, hipStream_t stream) {
+  constexpr int kBlockQ = 4 * 32 * kQT;
+  const int qblocks = (seq_q + kBlockQ - 1) / kBlockQ;
+  hipLaunchKernelGGL((flash_fwd<kD, kQT, kBK>), dim3((unsigned)(bh * qblocks)),
+                     dim3(kThreads), 0, stream, q, k, v, o, lse, heads, group,
+                     seq_q, seq_k, bh, qblocks, scale_log2, causal);
 }
 
 } // namespace
@@ -430,21 +580,19 @@ bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
     return false;
   }
   const int64_t bh = batch * heads;
-  const int64_t qblocks = (seq_q + kBlockQ - 1) / kBlockQ;
-  if (bh * qblocks > INT32_MAX || bh > INT32_MAX) {
+  /* One workgroup per 128 * kQT queries of a head; the grid stays within
+   * int32 for any accepted shape when it does for 128-query blocks. */
+  if (bh * ((seq_q + 127) / 128) > INT32_MAX || seq_k > INT32_MAX / 256) {
     return false;
   }
   const float scale_log2 = scale * 1.4426950408889634f;
   const int group = (int)(heads / kv_heads);
-  dim3 grid((unsigned)(bh * qblocks));
   if (head_dim == 128) {
-    hipLaunchKernelGGL((flash_fwd<128>), grid, dim3(kThreads), 0, stream, q, k,
-                       v, o, lse, (int)heads, group, (int)seq_q, (int)seq_k,
-                       (int)bh, (int)qblocks, scale_log2, causal);
+    launch<128, VX_FA_QT, VX_FA_BK>(q, k, v, o, lse, (int)heads, group, (int)seq_q,
+                          (int)seq_k, (int)bh, scale_log2, causal, stream);
   } else {
-    hipLaunchKernelGGL((flash_fwd<64>), grid, dim3(kThreads), 0, stream, q, k,
-                       v, o, lse, (int)heads, group, (int)seq_q, (int)seq_k,
-                       (int)bh, (int)qblocks, scale_log2, causal);
+    launch<64, VX_FA_QT, VX_FA_BK>(q, k, v, o, lse, (int)heads, group, (int)seq_q,
+                         (int)seq_k, (int)bh, scale_log2, causal, stream);
   }
   VX_HIP_CHECK(hipGetLastError());
   return true;

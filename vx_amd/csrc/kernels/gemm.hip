@@ -1,28 +1,27 @@
 /*
  * gemm.hip -- the routed `a @ b` on gfx950.
  *
- * Two kernels:
+ * 16-bit inputs (bf16 or f16), f32 accumulate, f32 or 16-bit output, on
+ * v_mfma_f32_32x32x16 tiles: one workgroup owns a 256x256 tile of C. The
+ * default kernel is gemm_mfma_dma (8 waves, two per SIMD): K is walked in
+ * stages of 32 through a 4-slot LDS ring filled by buffer-to-LDS loads three
+ * stages ahead; B keeps its global k-major order in LDS and reaches the MFMA
+ * through the transposing ds_read_b64_tr_b16. Workgroups are renumbered so
+ * the 32 consecutive tiles each XCD receives form a 4x8 patch of C, which
+ * keeps each XCD's A and B panels in its own L2.
  *
- *  - gemm_mfma_256: 16-bit inputs (bf16 or f16), f32 accumulate, f32 or
- *    16-bit output. One 256-thread workgroup (4 waves, 2x2) owns a 256x256
- *    tile of C and walks K in steps of 64. Each wave owns 128x128 of the tile
- *    as 4x4 v_mfma_f32_32x32x16 accumulators. A and B stages go through
- *    registers into a double-buffered LDS ring (2 x 64 KiB), one barrier per
- *    step. B arrives row-major (k-major), while the MFMA B operand wants
- *    8 consecutive k per lane, so each thread loads an 8x8 block of B and
- *    transposes it in registers before the LDS write; both LDS planes then
- *    hold 16-byte k-chunks per row, XOR-swizzled so ds_read_b128 of 16 rows
- *    at one k-chunk touch distinct banks. Workgroups are renumbered so that
- *    the 32 consecutive tiles each XCD receives form a 4x8 patch of C, which
- *    keeps each XCD's A and B panels in its own L2.
+ * Earlier register-staged variants (gemm_mfma_256, gemm_mfma_pipe with 4 or
+ * 8 waves, gemm_mfma_il) stay selectable for comparison and produce
+ * bit-identical results: every variant issues the same MFMAs on each
+ * accumulator in the same k order.
  *
- *  - gemm_tiled: every supported type pair, any shape and row stride. 64x64
- *    tiles, 16-deep K stages through LDS, one multiply and one add per term
- *    with contraction off, k in order: for f32 this is the same arithmetic,
- *    term for term, as the reference CPU loop nest
- *    (runtime/host_dispatch_common.h:65-79), and for bf16 -> f32 the same as
- *    the outlined linalg.matmul (extend, f32 multiply, f32 add, k sequential;
- *    src/codegen/flat/emit/tensor.rs:1600-1647).
+ * gemm_tiled takes every supported type pair, any shape and row stride:
+ * 64x64 tiles, 16-deep K stages through LDS, one multiply and one add per
+ * term with contraction off, k in order: for f32 this is the same
+ * arithmetic, term for term, as the reference CPU loop nest
+ * (runtime/host_dispatch_common.h:65-79), and for bf16 -> f32 the same as
+ * the outlined linalg.matmul (extend, f32 multiply, f32 add, k sequential;
+ * src/codegen/flat/emit/tensor.rs:1600-1647).
  */
 #include "../../../include/vx_hardware_runtime.h"
 #include "../vx_hip_common.h"
