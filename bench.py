@@ -15,8 +15,10 @@ The same JSON line carries:
     outlined-loop semantics, one thread) timed on a bounded block of rows of
     the same GEMM;
   - extra: flash-attention forward (config 3), int8 GEMV (config 5, weights
-    rotated through more than the 256 MB MALL) and int8 greedy decode
-    (config 4) when their paths are built.
+    rotated through more than the 256 MB MALL), int8 greedy decode
+    (config 4), the 8192^3 GEMM roofline point and the f32 512^3 plumbing
+    GEMM (config 1, with its parity against the oracle); with the CPU leg,
+    the oracle's own rate beside each of them on a bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu] [--only gemm,fa,gemv,decode]
 """
@@ -125,6 +127,111 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     ms_step = ms_events / steps
     return dict(n=n, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / steps,
                 tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16)
+
+
+def bench_gemm_f32(lib, timer, steps: int = 50, n: int = 512):
+    """BASELINE config 1 (the plumbing GEMM): f32 512^3, U[-1,1] operands,
+    through the ABI onto the exact-order tiled kernel. Reports the device
+    time per dispatch (hipEvents), the host wall time per dispatch, and the
+    largest relative error against the CPU oracle (the reference's loop)."""
+    import ctypes
+
+    import oracle
+    from vx_amd import abi
+    from vx_amd.runtime import DeviceArray
+
+    a = np.random.default_rng(1).uniform(-1, 1, (n, n)).astype(np.float32)
+    b = np.random.default_rng(2).uniform(-1, 1, (n, n)).astype(np.float32)
+    da, db = DeviceArray.of(lib, a, abi.DTYPE_F32), DeviceArray.of(lib, b, abi.DTYPE_F32)
+    dc = DeviceArray(lib, (n, n), abi.DTYPE_F32)
+    args = abi.CallArgs()
+    args.memref(da.descriptor(), abi.DTYPE_F32).scalar(0, abi.KIND_I64)
+    args.memref(db.descriptor(), abi.DTYPE_F32).scalar(1, abi.KIND_I64)
+    args.scalar(0.0, abi.KIND_F32).memref(dc.descriptor(), abi.DTYPE_F32)
+    pl = abi.matmul_payload(outkind="buffer")
+    buf = ctypes.create_string_buffer(pl, len(pl))
+    argv, tags, nargs = args.arrays()
+    dispatch = lib.lib.vx_plugin_dispatch_async
+
+    def one():
+        dispatch(buf, len(pl), argv, tags, nargs)
+
+    settle(one, timer, 50.0)
+    timer.sync()
+    e0, e1 = timer.event(), timer.event()
+    t0 = time.perf_counter()
+    timer.record(e0)
+    for _ in range(steps):
+        one()
+    timer.record(e1)
+    ms = timer.elapsed_ms(e0, e1) / steps
+    timer.sync()
+    wall_us = (time.perf_counter() - t0) / steps * 1e6
+    c = dc.numpy()
+    for x in (da, db, dc):
+        x.free()
+    t0 = time.perf_counter()
+    want = oracle.gemm_f32(a, b)
+    cpu_s = time.perf_counter() - t0
+    rel = float(np.max(np.abs(c - want) / np.maximum(1.0, np.abs(want))))
+    flops = 2.0 * n ** 3
+    return dict(config=f"f32 {n}^3, U[-1,1] seeds 1/2 (BASELINE config 1)", us=ms * 1e3,
+                wall_us_per_dispatch=wall_us, tflops=flops / (ms * 1e-3) / 1e12,
+                max_rel_err_vs_oracle=rel, parity_bound=1e-4,
+                cpu=dict(value=flops / cpu_s / 1e12, unit="TFLOP/s", cores=1, kind="port",
+                         sample=f"the whole {n}^3 GEMM, oracle/vx_oracle.c loop nest"))
+
+
+def cpu_fa(rows: int = 96):
+    """The CPU oracle's attention on `rows` query rows spread over config 3
+    (one thread); TFLOP/s over the exact causal work of those rows."""
+    import oracle
+    from vx_amd.abi import f32_to_bf16
+
+    b, h, s, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(7)
+    q, k, v = (f32_to_bf16(rng.standard_normal((b, h, s, d)).astype(np.float32)) for _ in range(3))
+    pick = np.random.default_rng(3)
+    sel = np.stack([pick.integers(0, b, rows), pick.integers(0, h, rows), pick.integers(0, s, rows)],
+                   axis=1).astype(np.int64)
+    t0 = time.perf_counter()
+    oracle.attention_rows(q, k, v, h, h, 1.0 / np.sqrt(d), True, sel)
+    dt = time.perf_counter() - t0
+    flops = float(np.sum(4.0 * d * (sel[:, 2] + 1)))
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="port",
+                sample=f"{rows} random query rows of causal [4,32,2048,128] ({flops / 1e9:.2f} GFLOP "
+                       f"in {dt:.2f} s), oracle/vx_oracle.c")
+
+
+def cpu_gemv(rows: int = 11008, cols: int = 4096):
+    import oracle
+    from vx_amd.abi import f32_to_bf16
+
+    rng = np.random.default_rng(11)
+    w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+    sc = rng.uniform(0.001, 0.01, rows).astype(np.float32)
+    x = f32_to_bf16(rng.standard_normal((1, cols)).astype(np.float32))
+    t0 = time.perf_counter()
+    oracle.gemv_i8(w, sc, x)
+    dt = time.perf_counter() - t0
+    return dict(value=rows * cols / dt / 1e9, unit="GB/s (weight bytes)", cores=1, kind="port",
+                sample=f"{rows}x{cols} batch 1, oracle/vx_oracle.c")
+
+
+def cpu_decode(n_steps: int = 8):
+    import oracle
+    from vx_amd.llama import CONFIG_DECODE, make_model, make_prompt
+
+    cfg = CONFIG_DECODE
+    model = make_model(cfg, seed=0)
+    prompt = make_prompt(cfg, n=16, seed=1)
+    t0 = time.perf_counter()
+    oracle.llama_generate(cfg.as_dict(), model, prompt, n_steps)
+    dt = time.perf_counter() - t0
+    positions = len(prompt) + n_steps - 1
+    return dict(value=positions / dt, unit="positions/s (= tok/s once past the prompt)", cores=1,
+                kind="port", sample=f"16-token prompt + {n_steps} greedy tokens of config 4 "
+                                    f"({positions} positions in {dt:.1f} s), oracle/vx_oracle.c")
 
 
 def bench_fa(lib, timer, steps: int, warmup: int):
@@ -288,11 +395,29 @@ def main() -> int:
             log("int8 decode config 4")
             extra["decode_i8"] = _decode.bench(lib, timer)
 
+    if "gemm" in only:
+        log("gemm bf16->f32 8192^3 (roofline point)")
+        g8 = bench_gemm(lib, timer, 10, 2, n=8192)
+        extra["gemm_bf16_8192"] = dict(config="bf16 x bf16 -> f32 GEMM, M=N=K=8192", ms=g8["ms_per_step"],
+                                       tflops=g8["tflops"], frac_of_peak=g8["tflops"] / PEAK_BF16_TFLOPS)
+        log(f"gemm 8192 {g8['tflops']:.1f} TFLOP/s")
+        log("gemm f32 512^3 (config 1)")
+        extra["gemm_f32_512"] = bench_gemm_f32(lib, timer)
+        log(f"gemm f32 512: {extra['gemm_f32_512']['us']:.1f} us device, "
+            f"{extra['gemm_f32_512']['wall_us_per_dispatch']:.1f} us per dispatch, "
+            f"max rel err {extra['gemm_f32_512']['max_rel_err_vs_oracle']:.2e}")
+
     cpu = None
     if not ns.skip_cpu:
         log("cpu baseline")
         cpu = cpu_baseline_gemm(g["a16"], g["b16"])
         cpu["nproc"] = os.cpu_count()
+        if "flash_attn_fwd" in extra:
+            extra["flash_attn_fwd"]["cpu"] = cpu_fa()
+        if "gemv_i8" in extra:
+            extra["gemv_i8_cpu"] = cpu_gemv()
+        if "decode_i8" in extra:
+            extra["decode_i8"]["cpu"] = cpu_decode()
 
     achieved = g["tflops"]
     line = {

@@ -35,6 +35,7 @@ struct LlamaI8 {
   float *att = nullptr, *hb = nullptr;
   int *pos = nullptr, *prompt = nullptr, *out_tokens = nullptr;
   float *out_margin = nullptr;
+  vxk::StepBest *best = nullptr; /* one per classifier workgroup */
   int prompt_cap = 0, out_cap = 0;
   hipStream_t stream = nullptr;
   std::vector<void *> owned;
@@ -173,8 +174,10 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
   lg.norm = m.rms_final;
   lg.out = m.logits;
   lg.pos = m.pos;
+  lg.part = m.best;
   vxk::step_gemv_logits(lg, m.stream);
-  vxk::step_argmax_launch(argmax_args(m, n_prompt), m.stream);
+  vxk::step_choose_launch(argmax_args(m, n_prompt), m.best,
+                          vxk::step_logits_groups(c.vocab_size), m.stream);
 }
 
 } // namespace
@@ -274,6 +277,7 @@ void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
   m->att = alloc<float>(*m, D);
   m->hb = alloc<float>(*m, H);
   m->pos = alloc<int>(*m, 1);
+  m->best = alloc<vxk::StepBest>(*m, (size_t)vxk::step_logits_groups(c.vocab_size));
   VX_HIP_CHECK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
   return m;
 }

@@ -13,9 +13,12 @@
  *   step_gemv<kSwiglu> RMSNorm(x), [W1; W3] GEMV with rows interleaved,
  *                      silu(h1) * h3
  *   step_gemv<kResid>  x += W2 h
- *   step_gemv<kLogits> final RMSNorm, classifier (the embedding table)
- *   step_argmax        argmax (lowest index wins a tie) or the next prompt
- *                      token; x = embedding of that token; pos += 1
+ *   step_gemv<kLogits> final RMSNorm, classifier (the embedding table);
+ *                      each workgroup also leaves the best and runner-up of
+ *                      its rows
+ *   step_choose        merges those: argmax (lowest index wins a tie) or the
+ *                      next prompt token; x = embedding of that token;
+ *                      pos += 1
  *
  * Every GEMV is weight-only int8 with one f32 scale per row over f32
  * activations (as in the reference, which is f32 throughout), f32 sums;
@@ -37,18 +40,57 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 256;
 constexpr int kMaxCols = 4096;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    v += __shfl_xor(v, off, 64);
+/* Wave-wide all-reduce with VALU data movement (DPP within 16-lane rows,
+ * v_permlane16/32_swap across them) instead of LDS-crossbar shuffles. */
+template <int kO> __device__ __forceinline__ float partner(float v) {
+  static_assert(kO == 1 || kO == 2 || kO == 4 || kO == 8, "within a row");
+  /* Lane i of a 16-lane row reads the lane differing in bit 3 (rotate by
+   * 8), bit 2 (mirror within 8), bit 1 or bit 0 (quad permutes). */
+  constexpr int ctrl = kO == 8 ? 0x128 : kO == 4 ? 0x141 : kO == 2 ? 0x4e : 0xb1;
+  return __uint_as_float(
+      __builtin_amdgcn_update_dpp(0u, __float_as_uint(v), ctrl, 0xf, 0xf, false));
+}
+
+/* Sum over groups of kN consecutive lanes (kN a power of two, <= 64); every
+ * lane of a group ends with its group's sum. */
+template <int kN> __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (kN >= 2) v += partner<1>(v);
+  if constexpr (kN >= 4) v += partner<2>(v);
+  if constexpr (kN >= 8) v += partner<4>(v);
+  if constexpr (kN >= 16) v += partner<8>(v);
+  if constexpr (kN >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                    __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (kN >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                    __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
   return v;
 }
 
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    v = fmaxf(v, __shfl_xor(v, off, 64));
+  v = fmaxf(v, partner<1>(v));
+  v = fmaxf(v, partner<2>(v));
+  v = fmaxf(v, partner<4>(v));
+  v = fmaxf(v, partner<8>(v));
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                    __float_as_uint(v), false,
+                                                    false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                    __float_as_uint(v), false,
+                                                    false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
   }
   return v;
 }
@@ -84,6 +126,51 @@ __device__ float block_max(float v, float *scratch) {
   return t;
 }
 
+/* Best and runner-up of a set of logits; i1 is the lowest index holding
+ * the best value. */
+using Best = StepBest;
+
+__device__ __forceinline__ Best merge(Best a, Best b) {
+  Best r;
+  if (b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1)) {
+    r.v1 = b.v1;
+    r.i1 = b.i1;
+    r.v2 = fmaxf(a.v1, b.v2);
+  } else {
+    r.v1 = a.v1;
+    r.i1 = a.i1;
+    r.v2 = fmaxf(a.v2, b.v1);
+  }
+  return r;
+}
+
+
+/* Classifier epilogue: the best and runner-up of this workgroup's rows
+ * into part[blockIdx.x], for step_choose to merge. */
+__device__ void logits_best(const StepGemvArgs &a, float acc0, float acc1,
+                            bool live, int r0) {
+  __shared__ Best wbest[kThreads / 64];
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  if (lane == 0) {
+    Best b{-INFINITY, 0x7fffffff, -INFINITY};
+    if (live) {
+      b = Best{a.scale[r0] * acc0, r0, -INFINITY};
+      b = merge(b, Best{a.scale[r0 + 1] * acc1, r0 + 1, -INFINITY});
+    }
+    wbest[wave] = b;
+  }
+  __syncthreads();
+  if (t == 0) {
+    Best b = wbest[0];
+    for (int w = 1; w < kThreads / 64; ++w) {
+      b = merge(b, wbest[w]);
+    }
+    a.part[blockIdx.x] = b;
+  }
+}
+
 enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3 };
 
 template <int kMode>
@@ -93,6 +180,27 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   __shared__ float scratch[kThreads / 64];
   const int t = threadIdx.x;
   const int cols = a.cols;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int r0 = (blockIdx.x * (kThreads / 64) + wave) * 2;
+  const bool live = r0 < a.rows;
+
+  /* The weights do not depend on x: request them first, so their latency
+   * runs under the normalisation below. */
+  constexpr int kSegs = kMaxCols / 1024;
+  u32x4 wp[kSegs], wq[kSegs];
+  {
+    const int8_t *w0 = a.w + (int64_t)(live ? r0 : 0) * cols;
+#pragma unroll
+    for (int s = 0; s < kSegs; ++s) {
+      const int c = s * 1024 + lane * 16;
+      const bool ok = live && c < cols;
+      wp[s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + c) : u32x4{0, 0, 0, 0};
+      wq[s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + cols + c)
+                 : u32x4{0, 0, 0, 0};
+    }
+  }
+
   if constexpr (kMode == kResid) {
     for (int i = t; i < cols; i += kThreads) {
       xin[i] = a.in[i];
@@ -112,28 +220,32 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   }
   __syncthreads();
 
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int r0 = (blockIdx.x * (kThreads / 64) + wave) * 2;
-  if (r0 >= a.rows) {
-    return;
-  }
-  const int8_t *w0 = a.w + (int64_t)r0 * cols;
-  const int8_t *w1 = w0 + cols;
   float acc0 = 0.0f, acc1 = 0.0f;
-  for (int c = lane * 16; c < cols; c += 64 * 16) {
-    const u32x4 p = *reinterpret_cast<const u32x4 *>(w0 + c);
-    const u32x4 q = *reinterpret_cast<const u32x4 *>(w1 + c);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float xv = xin[c + k];
-      acc0 += (float)(int8_t)(p[k >> 2] >> (8 * (k & 3))) * xv;
-      acc1 += (float)(int8_t)(q[k >> 2] >> (8 * (k & 3))) * xv;
+  for (int s = 0; s < kSegs; ++s) {
+    const int c = s * 1024 + lane * 16;
+    if (c < cols) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float xv = xin[c + k];
+        acc0 += (float)(int8_t)(wp[s][k >> 2] >> (8 * (k & 3))) * xv;
+        acc1 += (float)(int8_t)(wq[s][k >> 2] >> (8 * (k & 3))) * xv;
+      }
     }
   }
   acc0 = wave_sum(acc0);
   acc1 = wave_sum(acc1);
-  if (lane != 0) {
+  if constexpr (kMode == kLogits) {
+    if (lane == 0 && live) {
+      const float y0 = a.scale[r0] * acc0;
+      const float y1 = a.scale[r0 + 1] * acc1;
+      a.out[r0] = y0;
+      a.out[r0 + 1] = y1;
+    }
+    logits_best(a, acc0, acc1, live, r0);
+    return;
+  }
+  if (lane != 0 || !live) {
     return;
   }
   const float y0 = a.scale[r0] * acc0;
@@ -173,9 +285,6 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     val = val * (1.0f / (1.0f + expf(neg)));
     val = val * y1;
     a.hout[r0 >> 1] = val;
-  } else {
-    a.out[r0] = y0;
-    a.out[r0 + 1] = y1;
   }
 }
 
@@ -238,46 +347,23 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   }
 }
 
-struct Best {
-  float v1;  /* best value */
-  int i1;    /* its index (lowest among equals) */
-  float v2;  /* runner-up value */
-};
+constexpr int kChooseThreads = 1024;
 
-__device__ __forceinline__ Best merge(Best a, Best b) {
-  Best r;
-  if (b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1)) {
-    r.v1 = b.v1;
-    r.i1 = b.i1;
-    r.v2 = fmaxf(a.v1, b.v2);
-  } else {
-    r.v1 = a.v1;
-    r.i1 = a.i1;
-    r.v2 = fmaxf(a.v2, b.v1);
-  }
-  return r;
-}
-
-constexpr int kArgThreads = 1024;
-
-/* Argmax with strict '>' in index order (reference :160-171), or the next
- * prompt token while the prompt lasts; then the embedding of the chosen
- * token into x, and pos + 1. */
-__global__ __launch_bounds__(kArgThreads) void step_argmax(StepArgmaxArgs a) {
-  __shared__ Best part[kArgThreads / 64];
+/* Merge the classifier workgroups' partials: argmax with the lowest index
+ * winning a tie (reference examples/llama.vx:160-171), or the next prompt
+ * token while the prompt lasts; then x = the embedding of that token and
+ * pos + 1. */
+__global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
+                                                              const Best *part,
+                                                              int nparts) {
+  __shared__ Best merged[kChooseThreads / 64];
   __shared__ int chosen;
   const int t = threadIdx.x;
+  const int lane = t & 63;
   const int pos = *a.pos;
   Best b{-INFINITY, 0x7fffffff, -INFINITY};
-  for (int i = t; i < a.vocab; i += kArgThreads) {
-    const float v = a.logits[i];
-    if (v > b.v1) {
-      b.v2 = b.v1;
-      b.v1 = v;
-      b.i1 = i;
-    } else if (v > b.v2) {
-      b.v2 = v;
-    }
+  for (int i = t; i < nparts; i += kChooseThreads) {
+    b = merge(b, part[i]);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -287,14 +373,14 @@ __global__ __launch_bounds__(kArgThreads) void step_argmax(StepArgmaxArgs a) {
     o.v2 = __shfl_xor(b.v2, off, 64);
     b = merge(b, o);
   }
-  if ((t & 63) == 0) {
-    part[t >> 6] = b;
+  if (lane == 0) {
+    merged[t >> 6] = b;
   }
   __syncthreads();
   if (t == 0) {
-    Best r = part[0];
-    for (int w = 1; w < kArgThreads / 64; ++w) {
-      r = merge(r, part[w]);
+    Best r = merged[0];
+    for (int w = 1; w < kChooseThreads / 64; ++w) {
+      r = merge(r, merged[w]);
     }
     int tok;
     if (pos + 1 < a.n_prompt) {
@@ -312,7 +398,7 @@ __global__ __launch_bounds__(kArgThreads) void step_argmax(StepArgmaxArgs a) {
   __syncthreads();
   const int tok = chosen;
   const float s = a.tok_s[tok];
-  for (int i = t; i < a.dim; i += kArgThreads) {
+  for (int i = t; i < a.dim; i += kChooseThreads) {
     a.x[i] = (float)a.tok_q[(int64_t)tok * a.dim + i] * s;
   }
   if (t == 0) {
@@ -350,14 +436,20 @@ void step_gemv_resid(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kResid>
 void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kSwiglu>(a, s); }
 void step_gemv_logits(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kLogits>(a, s); }
 
+int step_logits_groups(int rows) {
+  return (rows / 2 + (kThreads / 64) - 1) / (kThreads / 64);
+}
+
+void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
+                        int nparts, hipStream_t s) {
+  hipLaunchKernelGGL(step_choose, dim3(1), dim3(kChooseThreads), 0, s, a, part,
+                     nparts);
+}
+
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
                            hipStream_t s) {
   hipLaunchKernelGGL(step_attention, dim3(heads), dim3(kThreads),
                      (size_t)seq_len * sizeof(float), s, a);
-}
-
-void step_argmax_launch(const StepArgmaxArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(step_argmax, dim3(1), dim3(kArgThreads), 0, s, a);
 }
 
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s) {

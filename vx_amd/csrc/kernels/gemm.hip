@@ -922,7 +922,9 @@ __device__ __forceinline__ void put_any(void *c, int64_t at, Acc v) {
   }
 }
 
-template <int kIn, int kOut>
+/* kT x kT output tile per workgroup (256 threads as 16 x 16, each with
+ * (kT/16)^2 outputs); kT shrinks for small grids so every CU gets work. */
+template <int kIn, int kOut, int kT>
 __global__ __launch_bounds__(256) void gemm_tiled(const void *__restrict__ A,
                                                   const void *__restrict__ B,
                                                   void *__restrict__ C,
@@ -931,45 +933,47 @@ __global__ __launch_bounds__(256) void gemm_tiled(const void *__restrict__ A,
                                                   int64_t ldb, int64_t ldc) {
 #pragma clang fp contract(off)
   using Acc = decltype(load_in<kIn>(nullptr, 0));
-  __shared__ Acc As[16][65]; /* [k][m] */
-  __shared__ Acc Bs[16][65]; /* [k][n] */
+  constexpr int kR = kT / 16;        /* outputs per thread per dimension */
+  constexpr int kLoads = kT * 16 / 256;
+  __shared__ Acc As[16][kT + 1]; /* [k][m] */
+  __shared__ Acc Bs[16][kT + 1]; /* [k][n] */
   const int t = threadIdx.x;
   const int tx = t & 15;
   const int ty = t >> 4;
-  const int64_t m0 = (int64_t)blockIdx.y * 64;
-  const int64_t n0 = (int64_t)blockIdx.x * 64;
-  Acc acc[4][4];
+  const int64_t m0 = (int64_t)blockIdx.y * kT;
+  const int64_t n0 = (int64_t)blockIdx.x * kT;
+  Acc acc[kR][kR];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < kR; ++i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kR; ++j) {
       acc[i][j] = Acc(0);
     }
   }
   for (int64_t k0 = 0; k0 < K; k0 += 16) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < kLoads; ++e) {
       const int idx = t + e * 256;
       const int am = idx >> 4, ak = idx & 15;
       const int64_t gm = m0 + am, gk = k0 + ak;
       As[ak][am] = (gm < M && gk < K) ? load_in<kIn>(A, gm * lda + gk) : Acc(0);
-      const int bk = idx >> 6, bn = idx & 63;
+      const int bk = idx / kT, bn = idx % kT;
       const int64_t hk = k0 + bk, hn = n0 + bn;
       Bs[bk][bn] = (hk < K && hn < N) ? load_in<kIn>(B, hk * ldb + hn) : Acc(0);
     }
     __syncthreads();
     const int kk_end = (K - k0) < 16 ? (int)(K - k0) : 16;
     for (int kk = 0; kk < kk_end; ++kk) {
-      Acc a[4], b[4];
+      Acc a[kR], b[kR];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = As[kk][ty * 4 + i];
-        b[i] = Bs[kk][tx * 4 + i];
+      for (int i = 0; i < kR; ++i) {
+        a[i] = As[kk][ty * kR + i];
+        b[i] = Bs[kk][tx * kR + i];
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < kR; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kR; ++j) {
           Acc prod = a[i] * b[j];
           acc[i][j] = acc[i][j] + prod;
         }
@@ -978,14 +982,14 @@ __global__ __launch_bounds__(256) void gemm_tiled(const void *__restrict__ A,
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t gm = m0 + ty * 4 + i;
+  for (int i = 0; i < kR; ++i) {
+    const int64_t gm = m0 + ty * kR + i;
     if (gm >= M) {
       continue;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t gn = n0 + tx * 4 + j;
+    for (int j = 0; j < kR; ++j) {
+      const int64_t gn = n0 + tx * kR + j;
       if (gn < N) {
         put_any<kOut>(C, gm * ldc + gn, acc[i][j]);
       }
@@ -1109,9 +1113,23 @@ void launch_il_any(const GemmArgs &g, hipStream_t s) {
 
 template <int kIn, int kOut>
 void launch_tiled(const GemmArgs &g, hipStream_t s) {
-  dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((g.m + 63) / 64));
-  hipLaunchKernelGGL((gemm_tiled<kIn, kOut>), grid, dim3(256), 0, s, g.a, g.b,
-                     g.c, g.m, g.n, g.k, g.lda, g.ldb, g.ldc);
+  /* The largest tile that still gives every CU (256 on gfx950) a workgroup;
+   * the arithmetic per output is the same at every tile size. */
+  const int64_t tiles64 = ((g.n + 63) / 64) * ((g.m + 63) / 64);
+  const int64_t tiles32 = ((g.n + 31) / 32) * ((g.m + 31) / 32);
+  if (tiles64 >= 256) {
+    dim3 grid((unsigned)((g.n + 63) / 64), (unsigned)((g.m + 63) / 64));
+    hipLaunchKernelGGL((gemm_tiled<kIn, kOut, 64>), grid, dim3(256), 0, s, g.a,
+                       g.b, g.c, g.m, g.n, g.k, g.lda, g.ldb, g.ldc);
+  } else if (tiles32 >= 256 || (g.m + 15) / 16 > 65535) {
+    dim3 grid((unsigned)((g.n + 31) / 32), (unsigned)((g.m + 31) / 32));
+    hipLaunchKernelGGL((gemm_tiled<kIn, kOut, 32>), grid, dim3(256), 0, s, g.a,
+                       g.b, g.c, g.m, g.n, g.k, g.lda, g.ldb, g.ldc);
+  } else {
+    dim3 grid((unsigned)((g.n + 15) / 16), (unsigned)((g.m + 15) / 16));
+    hipLaunchKernelGGL((gemm_tiled<kIn, kOut, 16>), grid, dim3(256), 0, s, g.a,
+                       g.b, g.c, g.m, g.n, g.k, g.lda, g.ldb, g.ldc);
+  }
 }
 
 } // namespace

@@ -12,29 +12,6 @@
 
 namespace vxk {
 
-struct StepGemvArgs {
-  const int8_t *w;     /* [rows, cols] */
-  const float *scale;  /* [rows] */
-  int rows, cols;
-  const float *x;      /* residual stream, normalised on the way in */
-  const float *norm;   /* RMSNorm weight */
-  const float *in;     /* input vector (residual mode) */
-  float *out;          /* q, x (accumulated) or logits */
-  float *hout;         /* SwiGLU output */
-  float *kcache, *vcache; /* this layer's [seq, kv_dim] */
-  const float *rope;   /* [seq, hs/2, 2] */
-  const int *pos;
-  int dim, kv_dim, hs;
-};
-
-struct StepAttnArgs {
-  const float *q;
-  const float *kcache, *vcache;
-  float *att;
-  const int *pos;
-  int kv_dim, hs, kv_mul;
-};
-
 struct StepArgmaxArgs {
   const float *logits;
   int vocab;
@@ -50,16 +27,53 @@ struct StepArgmaxArgs {
   int dim;
 };
 
+/* Best and runner-up logit of a workgroup's rows (classifier epilogue). */
+struct StepBest {
+  float v1;
+  int i1;
+  float v2;
+};
+
+struct StepGemvArgs {
+  const int8_t *w;     /* [rows, cols] */
+  const float *scale;  /* [rows] */
+  int rows, cols;
+  const float *x;      /* residual stream, normalised on the way in */
+  const float *norm;   /* RMSNorm weight */
+  const float *in;     /* input vector (residual mode) */
+  float *out;          /* q, x (accumulated) or logits */
+  float *hout;         /* SwiGLU output */
+  float *kcache, *vcache; /* this layer's [seq, kv_dim] */
+  const float *rope;   /* [seq, hs/2, 2] */
+  const int *pos;
+  int dim, kv_dim, hs;
+  /* Classifier only: one StepBest per workgroup. */
+  StepBest *part;
+};
+
+struct StepAttnArgs {
+  const float *q;
+  const float *kcache, *vcache;
+  float *att;
+  const int *pos;
+  int kv_dim, hs, kv_mul;
+};
+
+
 /* rows even, cols a multiple of 16 and at most 4096. */
 bool step_gemv_ok(int rows, int cols);
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s);
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s);
 void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s);
+/* The classifier; leaves step_logits_groups(rows) StepBest entries in
+ * `part` for step_choose_launch. */
 void step_gemv_logits(const StepGemvArgs &a, hipStream_t s);
+int step_logits_groups(int rows);
+void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
+                        int nparts, hipStream_t s);
 /* hs divides 256 and is at most 256; seq_len * 4 bytes of LDS. */
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
                            hipStream_t s);
-void step_argmax_launch(const StepArgmaxArgs &a, hipStream_t s);
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s);
 
 } // namespace vxk
