@@ -129,6 +129,37 @@ int32_t vx_llama_i8_logits(void *model, const int32_t *tokens, int32_t n,
 
 void vx_llama_i8_destroy(void *model);
 
+/* ---- Model files (host side; no GPU needed) ----
+ *
+ * Two formats are read:
+ *  - a llama2.c checkpoint, the file reference examples/llama.vx loads
+ *    (stdlib/rust_core/src/ffi/llama.rs:10-45 reads it: seven int32 --
+ *    dim, hidden_dim, n_layers, n_heads, n_kv_heads, vocab_size, seq_len --
+ *    then the f32 arrays in the order of examples/llama.vx:80-120; the
+ *    RoPE arrays llama2.c appends after rms_final may be present or not).
+ *    Every matrix is quantized per output row on the way in (scale =
+ *    max|w| / 127, q = round-half-even(w / scale));
+ *  - the int8 file vx_llama_i8_save writes ("VXQ8" version 1: the config,
+ *    then every array of vx_llama_i8_weights in field order, then a 64-bit
+ *    FNV-1a of everything before it), so the quantization is done once.
+ * Either way the RoPE table is computed from the config (base 10000), the
+ * classifier is the token table (a negative vocab_size -- an unshared
+ * classifier -- is refused), and the result feeds vx_llama_i8_create. */
+typedef struct vx_llama_i8_host vx_llama_i8_host;
+
+/* Read `path`; on VX_OP_OK, *cfg holds the config and *out the weights
+ * (free with vx_llama_i8_host_free). VX_OP_EINVAL for an unreadable,
+ * truncated or corrupt file, VX_OP_EUNSUPP for a layout this build does
+ * not take. */
+int32_t vx_llama_i8_read(const char *path, vx_llama_i8_config *cfg,
+                         vx_llama_i8_host **out);
+/* The weights of a read model, valid until vx_llama_i8_host_free. */
+const vx_llama_i8_weights *vx_llama_i8_host_weights(const vx_llama_i8_host *h);
+void vx_llama_i8_host_free(vx_llama_i8_host *h);
+/* Write cfg and w as a "VXQ8" file. */
+int32_t vx_llama_i8_save(const char *path, const vx_llama_i8_config *cfg,
+                         const vx_llama_i8_weights *w);
+
 #ifdef __cplusplus
 }
 #endif

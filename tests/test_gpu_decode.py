@@ -101,3 +101,29 @@ def test_refusals(hiplib):
     with pytest.raises(RuntimeError):
         model.generate([CONFIG_TINY.vocab_size], 4)  # token outside the vocabulary
     model.close()
+
+
+def test_model_read_from_checkpoint_file_generates_like_oracle(hiplib, tmp_path):
+    """A llama2.c checkpoint read through vx_llama_i8_read (quantized on the
+    way in), uploaded and run greedily, against the oracle on the same
+    weights; the VXQ8 file saved from it runs identically."""
+    from tests.test_llama_io import f32_model
+    from vx_amd.decode import read_model, save_model, write_checkpoint
+
+    announce("decode from a checkpoint file")
+    cfg = CONFIG_TINY
+    write_checkpoint(tmp_path / "tiny.bin", cfg, f32_model(cfg, seed=21))
+    rcfg, weights = read_model(hiplib, tmp_path / "tiny.bin")
+    assert rcfg == cfg
+    prompt = make_prompt(cfg, n=5, seed=8)
+    want, margin = oracle.llama_generate(cfg.as_dict(), weights, prompt, 30)
+    model = LlamaI8(hiplib, cfg, weights)
+    got, _ = model.generate(prompt, 30)
+    model.close()
+    assert_same_tokens(got, want, margin)
+    save_model(hiplib, tmp_path / "tiny.q8", cfg, weights)
+    _, again = read_model(hiplib, tmp_path / "tiny.q8")
+    model = LlamaI8(hiplib, cfg, again)
+    got2, _ = model.generate(prompt, 30)
+    model.close()
+    assert list(map(int, got2)) == list(map(int, got))

@@ -1,0 +1,127 @@
+"""Model files for the int8 decode path (vx_llama_i8_read / _save): the
+reference's llama2.c checkpoint layout, quantized on the way in, and the
+build's VXQ8 int8 file. Host-side only: runs without a GPU."""
+
+import numpy as np
+import pytest
+
+import oracle
+from vx_amd import llama
+from vx_amd.decode import read_model, save_model, write_checkpoint
+from vx_amd.runtime import DispatchLibrary
+
+CFG = llama.CONFIG_TINY
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return DispatchLibrary(hip=True)
+
+
+def f32_model(cfg, seed=5):
+    rng = np.random.default_rng(seed)
+    d, h, kv, L = cfg.dim, cfg.hidden_dim, cfg.kv_dim, cfg.n_layers
+
+    def mat(*shape):
+        return (rng.standard_normal(shape) * 0.02).astype(np.float32)
+
+    m = {"tok": mat(cfg.vocab_size, d), "wq": mat(L, d, d), "wk": mat(L, kv, d),
+         "wv": mat(L, kv, d), "wo": mat(L, d, d), "w1": mat(L, h, d), "w2": mat(L, d, h),
+         "w3": mat(L, h, d)}
+    m["rms_att"] = rng.uniform(0.5, 1.5, (L, d)).astype(np.float32)
+    m["rms_ffn"] = rng.uniform(0.5, 1.5, (L, d)).astype(np.float32)
+    m["rms_final"] = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    m["tok"][3, :] = 0.0  # a zero row: scale 1, all-zero codes
+    return m
+
+
+def expected(cfg, m):
+    """The checker's quantization of the same f32 arrays."""
+    want = {}
+    for name in ("tok", "wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+        w = m[name]
+        q, s = oracle.quantize_rows(w.reshape(-1, w.shape[-1]))
+        key = "tok" if name == "tok" else name
+        want[f"{key}_q"] = q.reshape(w.shape)
+        want[f"{key}_s"] = s.reshape(w.shape[:-1])
+    for name in ("rms_att", "rms_ffn", "rms_final"):
+        want[name] = m[name]
+    want["rope"] = llama.rope_table(cfg)
+    return want
+
+
+@pytest.mark.parametrize("rope_arrays", [True, False])
+def test_checkpoint_quantized_like_the_checker(lib, tmp_path, rope_arrays):
+    m = f32_model(CFG)
+    path = tmp_path / "tiny.bin"
+    write_checkpoint(path, CFG, m, rope_arrays=rope_arrays)
+    cfg, got = read_model(lib, path)
+    assert cfg == CFG
+    want = expected(CFG, m)
+    for name, arr in want.items():
+        assert np.array_equal(got[name], arr), name
+    assert not got["tok_q"][3].any() and got["tok_s"][3] == 1.0
+
+
+def test_quantizer_agrees_with_numpy_restatement():
+    """The checker's C quantizer against the numpy statement of the same rule
+    (scale = max|w|/127, round half to even), including exact ties."""
+    w = np.array([[127.0, 63.5, -0.5, 1.5, 2.5, -127.0]], np.float32)
+    q, s = oracle.quantize_rows(w)
+    assert s[0] == 1.0 and list(q[0]) == [127, 64, 0, 2, 2, -127]
+    w = np.random.default_rng(0).standard_normal((64, 96)).astype(np.float32)
+    q, s = oracle.quantize_rows(w)
+    qn, sn = llama.quantize_rows(w)
+    assert np.array_equal(q, qn) and np.array_equal(s, sn)
+
+
+def test_q8_round_trip(lib, tmp_path):
+    m = llama.make_model(CFG, seed=3)
+    path = tmp_path / "tiny.q8"
+    save_model(lib, path, CFG, m)
+    cfg, got = read_model(lib, path)
+    assert cfg == CFG
+    for name in m:
+        assert np.array_equal(got[name], m[name]), name
+    # The file is the config plus every stored array, nothing else.
+    stored = sum(a.nbytes for k, a in m.items() if k != "rope")
+    assert path.stat().st_size == 8 + 28 + stored + 8
+
+
+def test_checkpoint_then_q8_gives_the_same_model(lib, tmp_path):
+    m = f32_model(CFG, seed=9)
+    write_checkpoint(tmp_path / "a.bin", CFG, m)
+    cfg, first = read_model(lib, tmp_path / "a.bin")
+    save_model(lib, tmp_path / "a.q8", cfg, first)
+    _, second = read_model(lib, tmp_path / "a.q8")
+    for name in first:
+        assert np.array_equal(first[name], second[name]), name
+
+
+def test_refusals(lib, tmp_path):
+    m = f32_model(CFG)
+    good = tmp_path / "good.bin"
+    write_checkpoint(good, CFG, m)
+    data = good.read_bytes()
+    with pytest.raises(OSError):
+        read_model(lib, tmp_path / "missing.bin")
+    (tmp_path / "short.bin").write_bytes(data[:-4])
+    with pytest.raises(OSError):
+        read_model(lib, tmp_path / "short.bin")
+    neg = bytearray(data)
+    neg[20:24] = np.int32(-CFG.vocab_size).tobytes()  # unshared classifier
+    (tmp_path / "neg.bin").write_bytes(bytes(neg))
+    with pytest.raises(OSError) as e:
+        read_model(lib, tmp_path / "neg.bin")
+    assert e.value.args[0] == -4  # VX_OP_EUNSUPP
+    bad = bytearray(data)
+    bad[12:16] = np.int32(5).tobytes()  # n_heads 5 does not divide dim 64
+    (tmp_path / "bad.bin").write_bytes(bytes(bad))
+    with pytest.raises(OSError):
+        read_model(lib, tmp_path / "bad.bin")
+    save_model(lib, tmp_path / "m.q8", CFG, llama.make_model(CFG))
+    q8 = bytearray((tmp_path / "m.q8").read_bytes())
+    q8[100] ^= 1
+    (tmp_path / "flip.q8").write_bytes(bytes(q8))
+    with pytest.raises(OSError):
+        read_model(lib, tmp_path / "flip.q8")

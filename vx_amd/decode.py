@@ -3,6 +3,7 @@
     model = LlamaI8(lib, cfg, weights)     # upload (weights from vx_amd.llama)
     tokens, margin = model.generate(prompt, n_steps)
     logits = model.logits(tokens)          # per position, for parity checks
+    cfg, weights = read_model(lib, path)   # a llama2.c checkpoint or VXQ8 file
 """
 
 from __future__ import annotations
@@ -27,6 +28,77 @@ class _Config(ctypes.Structure):
 
 class _Weights(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in WEIGHT_FIELDS]
+
+
+def _shapes(cfg: LlamaConfig) -> dict[str, tuple[tuple[int, ...], type]]:
+    d, h, kv, L, hs = cfg.dim, cfg.hidden_dim, cfg.kv_dim, cfg.n_layers, cfg.head_size
+    i8, f32 = np.int8, np.float32
+    return {
+        "tok_q": ((cfg.vocab_size, d), i8), "tok_s": ((cfg.vocab_size,), f32),
+        "rms_att": ((L, d), f32),
+        "wq_q": ((L, d, d), i8), "wq_s": ((L, d), f32),
+        "wk_q": ((L, kv, d), i8), "wk_s": ((L, kv), f32),
+        "wv_q": ((L, kv, d), i8), "wv_s": ((L, kv), f32),
+        "wo_q": ((L, d, d), i8), "wo_s": ((L, d), f32),
+        "rms_ffn": ((L, d), f32),
+        "w1_q": ((L, h, d), i8), "w1_s": ((L, h), f32),
+        "w2_q": ((L, d, h), i8), "w2_s": ((L, d), f32),
+        "w3_q": ((L, h, d), i8), "w3_s": ((L, h), f32),
+        "rms_final": ((d,), f32), "rope": ((cfg.seq_len, hs // 2, 2), f32),
+    }
+
+
+def read_model(lib, path) -> tuple[LlamaConfig, dict[str, np.ndarray]]:
+    """Read a llama2.c checkpoint (quantized on the way in) or a VXQ8 file
+    through vx_llama_i8_read; returns the config and numpy copies of the
+    weights, keyed as make_model's."""
+    c = _Config()
+    h = ctypes.c_void_p()
+    rc = lib.lib.vx_llama_i8_read(str(path).encode(), ctypes.byref(c), ctypes.byref(h))
+    if rc != 0:
+        raise OSError(rc, f"vx_llama_i8_read refused {path}")
+    try:
+        cfg = LlamaConfig(**{n: getattr(c, n) for n, _ in _Config._fields_})
+        w = _Weights.from_address(lib.lib.vx_llama_i8_host_weights(h))
+        out = {}
+        for name, (shape, dtype) in _shapes(cfg).items():
+            n = int(np.prod(shape))
+            buf = (ctypes.c_char * (n * np.dtype(dtype).itemsize)).from_address(getattr(w, name))
+            out[name] = np.frombuffer(bytes(buf), dtype=dtype).reshape(shape)
+    finally:
+        lib.lib.vx_llama_i8_host_free(h)
+    return cfg, out
+
+
+def save_model(lib, path, cfg: LlamaConfig, weights: dict) -> None:
+    """Write weights (keyed as make_model's) as a VXQ8 file."""
+    c = _Config(**cfg.as_dict())
+    w = _Weights()
+    keep = []
+    for name in WEIGHT_FIELDS:
+        arr = np.ascontiguousarray(weights[name])
+        keep.append(arr)
+        setattr(w, name, arr.ctypes.data)
+    rc = lib.lib.vx_llama_i8_save(str(path).encode(), ctypes.byref(c), ctypes.byref(w))
+    if rc != 0:
+        raise OSError(rc, f"vx_llama_i8_save refused {path}")
+
+
+def write_checkpoint(path, cfg: LlamaConfig, f32: dict[str, np.ndarray], rope_arrays: bool = True) -> None:
+    """A llama2.c checkpoint of f32 weights (keys tok, rms_att, wq, wk, wv,
+    wo, rms_ffn, w1, w2, w3, rms_final): the seven-int header, the arrays in
+    the reference's order, and (as llama2.c writes them) the RoPE cos/sin
+    arrays it leaves unread."""
+    hdr = np.array([cfg.dim, cfg.hidden_dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads,
+                    cfg.vocab_size, cfg.seq_len], np.int32)
+    with open(path, "wb") as f:
+        f.write(hdr.tobytes())
+        for name in ("tok", "rms_att", "wq", "wk", "wv", "wo", "rms_ffn", "w1", "w2", "w3",
+                     "rms_final"):
+            f.write(np.ascontiguousarray(f32[name], np.float32).tobytes())
+        if rope_arrays:
+            half = cfg.seq_len * cfg.head_size // 2
+            f.write(np.zeros(2 * half, np.float32).tobytes())
 
 
 class LlamaI8:

@@ -68,6 +68,10 @@ HIP_SIGNATURES = {
     "vx_llama_i8_generate": (_i32, [_vp, _vp, _i32, _i32, _vp, _vp, _i32]),
     "vx_llama_i8_logits": (_i32, [_vp, _vp, _i32, _vp]),
     "vx_llama_i8_destroy": (None, [_vp]),
+    "vx_llama_i8_read": (_i32, [ctypes.c_char_p, _vp, ctypes.POINTER(_vp)]),
+    "vx_llama_i8_host_weights": (_vp, [_vp]),
+    "vx_llama_i8_host_free": (None, [_vp]),
+    "vx_llama_i8_save": (_i32, [ctypes.c_char_p, _vp, _vp]),
 }
 
 
