@@ -265,6 +265,42 @@ def test_mfma_variants_bit_identical(hiplib, out_dt, rng):
         assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-3)
 
 
+@pytest.mark.parametrize("k", [64, 128, 192, 768])
+@pytest.mark.parametrize("out_dt", [abi.DTYPE_F32, abi.DTYPE_BF16])
+def test_mfma_pp_against_oracle(hiplib, k, out_dt, rng):
+    """The ping-pong kernel adds 32-term MFMA sums where the other MFMA
+    kernels add 16-term ones, so it is held to the oracle and to f64 instead
+    of to them bit for bit, at K of 2, 4 and 6 stages (the ring's prologue
+    and tail cases) and 24; and it is deterministic across calls."""
+    announce(f"gemm mfma ping-pong k={k} out={out_dt}")
+    a16 = f32_to_bf16(rng.normal(0, 1, (512, k)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1, (k, 768)).astype(np.float32))
+    c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, out_dt, kernel=abi.GEMM_MFMA_PP)
+    assert st["gemm_mfma"] == 1
+    again, _ = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, out_dt, kernel=abi.GEMM_MFMA_PP)
+    assert np.array_equal(c, again)
+    want = oracle.gemm_bf16_f32(a16, b16)
+    exact = bf16_to_f32(a16).astype(np.float64) @ bf16_to_f32(b16).astype(np.float64)
+    if out_dt == abi.DTYPE_F32:
+        assert_max_abs(c, want, 1e-3, "ping-pong vs oracle")
+        assert np.abs(c - exact).max() <= 1e-5 * max(1.0, np.abs(exact).max())
+    else:
+        got = bf16_to_f32(c)
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-3)
+
+
+def test_mfma_pp_f16(hiplib, rng):
+    """f16 operands through the ping-pong kernel's f16 MFMA."""
+    announce("gemm mfma ping-pong f16")
+    a = rng.normal(0, 1, (256, 256)).astype(np.float16)
+    b = rng.normal(0, 1, (256, 512)).astype(np.float16)
+    c, st = gpu_gemm(hiplib, a.view(np.uint16), b.view(np.uint16), abi.DTYPE_F16, abi.DTYPE_F32,
+                     kernel=abi.GEMM_MFMA_PP)
+    assert st["gemm_mfma"] == 1
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(c - exact).max() <= 1e-5 * np.abs(exact).max()
+
+
 def test_flat_matvec(hiplib, rng):
     """vx_plugin_dispatch_async_flat: xout[i] = sum_j w[i*n+j] x[j]."""
     announce("flat matvec")

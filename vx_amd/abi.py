@@ -41,8 +41,8 @@ CTRL_VENDOR_BASE = 0x1000
 HIP_CTRL_GEMM_KERNEL = CTRL_VENDOR_BASE + 1
 HIP_CTRL_STATS = CTRL_VENDOR_BASE + 2
 HIP_CTRL_POOL_DRAIN = CTRL_VENDOR_BASE + 3
-GEMM_AUTO, GEMM_MFMA, GEMM_TILED, GEMM_MFMA_PIPE4, GEMM_MFMA_PIPE8, GEMM_MFMA_IL, GEMM_MFMA_DMA, GEMM_MFMA_DMA8 = (
-    0, 1, 2, 3, 4, 5, 6, 7)
+(GEMM_AUTO, GEMM_MFMA, GEMM_TILED, GEMM_MFMA_PIPE4, GEMM_MFMA_PIPE8, GEMM_MFMA_IL, GEMM_MFMA_DMA,
+ GEMM_MFMA_DMA8, GEMM_MFMA_PP) = (0, 1, 2, 3, 4, 5, 6, 7, 8)
 
 
 def memref_tag(dtype: int, rank: int) -> int:

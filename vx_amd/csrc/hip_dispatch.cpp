@@ -727,9 +727,10 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     /* payload -> int32_t: 0 automatic, 1 MFMA (plain), 2 tiled, 3 MFMA
      * pipelined on 4 waves, 4 MFMA pipelined on 8 waves, 5 MFMA with the
      * non-MFMA work interleaved, 6/7 MFMA with direct-to-LDS loads (4 or 8
-     * waves). */
+     * waves), 8 the same loads with SIMD-sharing waves taking turns on
+     * 16x16x32 MFMAs. */
     const int32_t *which = static_cast<const int32_t *>(payload);
-    if (!which || *which < 0 || *which > 7) {
+    if (!which || *which < 0 || *which > 8) {
       return 0;
     }
     forced_gemm_kernel.store(*which);

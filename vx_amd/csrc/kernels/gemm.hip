@@ -2,18 +2,21 @@
  * gemm.hip -- the routed `a @ b` on gfx950.
  *
  * 16-bit inputs (bf16 or f16), f32 accumulate, f32 or 16-bit output, on
- * v_mfma_f32_32x32x16 tiles: one workgroup owns a 256x256 tile of C. The
- * default kernel is gemm_mfma_dma (8 waves, two per SIMD): K is walked in
- * stages of 32 through a 4-slot LDS ring filled by buffer-to-LDS loads three
- * stages ahead; B keeps its global k-major order in LDS and reaches the MFMA
- * through the transposing ds_read_b64_tr_b16. Workgroups are renumbered so
- * the 32 consecutive tiles each XCD receives form a 4x8 patch of C, which
+ * MFMA tiles: one workgroup owns a 256x256 tile of C. The default kernel is
+ * gemm_mfma_pp (8 waves, two per SIMD, on v_mfma_f32_16x16x32): K is walked
+ * in stages of 32 through a 4-slot LDS ring filled by buffer-to-LDS loads
+ * three stages ahead; B keeps its global k-major order in LDS and reaches the
+ * MFMA through the transposing ds_read_b64_tr_b16; the two waves that share
+ * a SIMD alternate between loading operands and computing, so the MFMA pipe,
+ * the LDS and the load path work at the same time. Workgroups are renumbered
+ * so the 32 consecutive tiles each XCD receives form a 4x8 patch of C, which
  * keeps each XCD's A and B panels in its own L2.
  *
- * Earlier register-staged variants (gemm_mfma_256, gemm_mfma_pipe with 4 or
- * 8 waves, gemm_mfma_il) stay selectable for comparison and produce
- * bit-identical results: every variant issues the same MFMAs on each
- * accumulator in the same k order.
+ * Earlier variants on v_mfma_f32_32x32x16 (gemm_mfma_256, gemm_mfma_pipe
+ * with 4 or 8 waves, gemm_mfma_il, gemm_mfma_dma with 4 or 8 waves) stay
+ * selectable for comparison and produce bit-identical results among
+ * themselves: every one issues the same MFMAs on each accumulator in the
+ * same k order.
  *
  * gemm_tiled takes every supported type pair, any shape and row stride:
  * 64x64 tiles, 16-deep K stages through LDS, one multiply and one add per
@@ -686,6 +689,207 @@ __global__ __launch_bounds__(64 * kWM * kWN, 1) void gemm_mfma_dma(
   }
 }
 
+/* Ping-pong variant on v_mfma_f32_16x16x32: the same 256x256 tile, the same
+ * 4-slot ring of K=32 stages filled by buffer-to-LDS loads, 8 waves (2x4,
+ * 128x64 of C each), and the two waves that share a SIMD take turns.
+ *
+ * The waves with wm = 0 (one per SIMD) form group 0, those with wm = 1
+ * group 1. Each wave alternates a load phase (issue its share of the DMA
+ * three stages ahead, read all operands of its next stage from LDS, wait for
+ * them) and a compute phase (the stage's 32 MFMAs, from registers). Group 1
+ * starts one phase late, so on every SIMD one wave computes while the other
+ * loads, and the MFMA pipe, the LDS and the load path are busy at the same
+ * time instead of in turns. A workgroup barrier separates the phases; group
+ * 1's extra barrier at the start is matched by group 0's at the end, after
+ * its epilogue, so every wave executes the same number of barriers.
+ *
+ * Ring invariants (phase p of the barrier sequence: group 0 loads stage j in
+ * phase 2j and computes it in 2j+1; group 1 loads it in 2j+1 and computes it
+ * in 2j+2): stage j+3 is issued by group 0 in phase 2j and by group 1 in
+ * phase 2j+1 into slot (j+3) % 4, whose previous stage j-1 was last read in
+ * phase 2j-1 (every wave drains its LDS reads before each barrier); each wave
+ * waits for its share of stage j+1 before the barrier that opens phase 2j+2,
+ * the first phase that reads it.
+ *
+ * The 16x16x32 MFMA takes a whole stage's k in one instruction and draws
+ * less power per flop than 32x32x16 on random operands (about 2.09 against
+ * 1.85 PFLOP/s sustained when MFMA-bound on this part), which is what bounds
+ * this kernel. A operands are one ds_read_b128 per 16x32 block (lane l: row
+ * l%16, k chunk l/16); B operands two ds_read_b64_tr_b16 per 32x16 block.
+ * B's LDS chunk swizzle also folds in bit 3 of k, so the four k chunks one
+ * transposing read touches land in distinct banks. Each accumulator adds its
+ * 32-term stage sums in k order, so results are deterministic (not
+ * bit-identical to the 32x32x16 kernels, which add 16-term sums). */
+__device__ __forceinline__ int pswz_b(int k, int c) {
+  return c ^ (((k & 3) | (((k >> 3) & 1) << 2)) << 1);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool kBf16>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+        0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+        0);
+  }
+}
+
+template <bool kBf16, int kOut>
+__global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
+    int tiles_m, int tiles_n) {
+  constexpr int kNS = 4;
+  constexpr int kLoads = kDUnits / 64 / 8; /* per wave per plane */
+  constexpr int kTM = 8;                   /* 16-row blocks per wave */
+  constexpr int kTN = 4;                   /* 16-column blocks per wave */
+  __shared__ u32x4 ring[kNS][2][kDUnits];
+
+  const int t = threadIdx.x;
+  int id = blockIdx.x;
+  const int nwg = gridDim.x;
+  if ((nwg & 7) == 0) {
+    id = (id & 7) * (nwg >> 3) + (id >> 3);
+  }
+  const int group_size = kGroupM * tiles_n;
+  const int first_m = (id / group_size) * kGroupM;
+  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int in_group = id % group_size;
+  const int tm = first_m + in_group % rows_in_group;
+  const int tn = in_group / rows_in_group;
+  const int64_t m0 = (int64_t)tm * kTileM;
+  const int64_t n0 = (int64_t)tn * kTileN;
+
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63;
+
+  uint32_t a_off[kLoads], b_off[kLoads];
+#pragma unroll
+  for (int p = 0; p < kLoads; ++p) {
+    const int u = (wave * kLoads + p) * 64 + lane;
+    const int arow = u >> 2;
+    a_off[p] = (uint32_t)(arow * lda * 2 + dswz_a(arow, u & 3) * 16);
+    const int bk = u >> 5;
+    b_off[p] = (uint32_t)(bk * ldb * 2 + pswz_b(bk, u & 31) * 16);
+  }
+  const int a_bytes = (int)((kTileM - 1) * lda * 2 + kDStageK * 2);
+  const int b_bytes = (int)((kDStageK - 1) * ldb * 2 + kTileN * 2);
+
+  const uint32_t ring_base =
+      (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
+  auto issue = [&](int step, int slot) {
+    const i32x4 ra =
+        buffer_rsrc(A + m0 * lda + (int64_t)step * kDStageK, a_bytes);
+    const i32x4 rb =
+        buffer_rsrc(B + (int64_t)step * kDStageK * ldb + n0, b_bytes);
+    const uint32_t la = ring_base + (uint32_t)(slot * 2 * kDUnits * 16) +
+                        (uint32_t)(wave * kLoads * 64 * 16);
+#pragma unroll
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(ra, a_off[p], la + p * 64 * 16);
+    }
+#pragma unroll
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(rb, b_off[p], la + kDUnits * 16 + p * 64 * 16);
+    }
+  };
+
+  f32x4 acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+
+  const int wm = wave >> 2; /* also the group */
+  const int wn = wave & 3;
+  const int l16 = lane & 15;
+  const int kc = lane >> 4; /* k chunk of this lane's operands */
+
+  auto frags = [&](int slot, u32x4 (&af)[kTM], u32x4 (&bfr)[kTN]) {
+    const u32x4 *la = ring[slot][0];
+    const VX_LDS char *lb = (const VX_LDS char *)&ring[slot][1][0];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const int row = wm * 128 + i * 16 + l16;
+      af[i] = la[row * 4 + dswz_a(row, kc)];
+    }
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int n = wn * 64 + j * 16 + 4 * (l16 & 3);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 8 * kc + 4 * h + (l16 >> 2);
+        const int at = k * (kTileN * 2) + pswz_b(k, n >> 3) * 16 + (n & 7) * 2;
+        const u32x2 w = __builtin_bit_cast(
+            u32x2,
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS i16x4 *)(lb + at)));
+        bfr[j][2 * h] = w[0];
+        bfr[j][2 * h + 1] = w[1];
+      }
+    }
+  };
+
+  const int steps = K / kDStageK;
+#pragma unroll
+  for (int s = 0; s < kNS - 1; ++s) {
+    if (s < steps) {
+      issue(s, s);
+    }
+  }
+  wait_stages<kNS - 2, 2 * kLoads>(min(steps - 1, kNS - 2));
+  lds_barrier();
+  if (wm == 1) {
+    lds_barrier();
+  }
+  u32x4 af[kTM], bfr[kTN];
+  for (int j = 0; j < steps; ++j) {
+    /* load phase */
+    if (j + kNS - 1 < steps) {
+      issue(j + kNS - 1, (j + kNS - 1) % kNS);
+    }
+    frags(j % kNS, af, bfr);
+    if (j + 1 < steps) {
+      wait_stages<kNS - 2, 2 * kLoads>(min(steps - 2 - j, kNS - 2));
+    }
+    lds_barrier();
+    /* compute phase */
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int jj = 0; jj < kTN; ++jj) {
+        acc[i][jj] = mfma16<kBf16>(af[i], bfr[jj], acc[i][jj]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  }
+
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < kTN; ++jj) {
+      const int64_t col = n0 + wn * 64 + jj * 16 + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + wm * 128 + i * 16 + 4 * kc + r;
+        put<kOut>(C, row * ldc + col, acc[i][jj][r]);
+      }
+    }
+  }
+  if (wm == 0) {
+    lds_barrier(); /* matches group 1's extra barrier before the loop */
+  }
+}
+
 /* Interleaved variant: the same tile, the same LDS layout and the same MFMA
  * order (so bit-identical results), with every non-MFMA instruction of a
  * stage issued in the shadow of an MFMA. With one wave per SIMD the MFMA
@@ -1087,6 +1291,26 @@ void launch_dma(const GemmArgs &g, hipStream_t s) {
                      g.ldb, g.ldc, tiles_m, tiles_n);
 }
 
+template <bool kBf16, int kOut>
+void launch_pp(const GemmArgs &g, hipStream_t s) {
+  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
+  hipLaunchKernelGGL((gemm_mfma_pp<kBf16, kOut>), dim3(tiles_m * tiles_n),
+                     dim3(512), 0, s, static_cast<const uint16_t *>(g.a),
+                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
+                     g.ldb, g.ldc, tiles_m, tiles_n);
+}
+
+void launch_pp_any(const GemmArgs &g, hipStream_t s) {
+  const bool bf = g.in_dtype == VX_DTYPE_BF16;
+  if (g.out_dtype == VX_DTYPE_F32) {
+    bf ? launch_pp<true, VX_DTYPE_F32>(g, s) : launch_pp<false, VX_DTYPE_F32>(g, s);
+  } else if (bf) {
+    launch_pp<true, VX_DTYPE_BF16>(g, s);
+  } else {
+    launch_pp<false, VX_DTYPE_F16>(g, s);
+  }
+}
+
 template <int kWM, int kWN>
 void launch_dma_any(const GemmArgs &g, hipStream_t s) {
   const bool bf = g.in_dtype == VX_DTYPE_BF16;
@@ -1136,7 +1360,7 @@ void launch_tiled(const GemmArgs &g, hipStream_t s) {
 
 GemmKernel gemm_pick(const GemmArgs &g) {
   if (dma_takes(g)) {
-    return GEMM_MFMA_DMA8;
+    return GEMM_MFMA_PP;
   }
   if (mfma_takes(g)) {
     return GEMM_MFMA_PIPE4;
@@ -1183,6 +1407,11 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
       return false;
     }
     launch_dma_any<2, 4>(g, stream);
+  } else if (which == GEMM_MFMA_PP) {
+    if (!dma_takes(g)) {
+      return false;
+    }
+    launch_pp_any(g, stream);
   } else if (which == GEMM_TILED) {
     if (!tiled_takes(g)) {
       return false;

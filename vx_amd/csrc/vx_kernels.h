@@ -37,12 +37,13 @@ enum GemmKernel {
   GEMM_MFMA_IL = 5,    /* as 1, every non-MFMA instruction in MFMA shadow */
   GEMM_MFMA_DMA = 6,   /* as 1, global -> LDS direct, 4-deep ring of K=32 */
   GEMM_MFMA_DMA8 = 7,  /* as 6, 8 waves (two per SIMD) */
+  GEMM_MFMA_PP = 8,    /* as 7 on 16x16x32 MFMAs, SIMD-sharing waves alternate */
 };
 
 inline bool gemm_is_mfma(GemmKernel k) {
   return k == GEMM_MFMA_256 || k == GEMM_MFMA_PIPE4 || k == GEMM_MFMA_PIPE8 ||
          k == GEMM_MFMA_IL || k == GEMM_MFMA_DMA ||
-         k == GEMM_MFMA_DMA8;
+         k == GEMM_MFMA_DMA8 || k == GEMM_MFMA_PP;
 }
 
 GemmKernel gemm_pick(const GemmArgs &g);
