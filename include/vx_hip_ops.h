@@ -160,6 +160,27 @@ void vx_llama_i8_host_free(vx_llama_i8_host *h);
 int32_t vx_llama_i8_save(const char *path, const vx_llama_i8_config *cfg,
                          const vx_llama_i8_weights *w);
 
+/* ---- device images in the payload ------------------------------------
+ *
+ * vx_plugin_dispatch_async runs a region whose payload says `format=hsaco`
+ * from the gfx950 code object in the payload's binary section (a bare ELF or
+ * a clang offload bundle): one parameter per memref field (allocated,
+ * aligned, offset, sizes, strides) and per scalar, as the reference's PTX
+ * path marshals them (runtime/vx_kernel_launch.h:57-140); the launch shape
+ * from `grid=`/`block=`/`grid_loops=` or `launch=`; `assert_flag=1` appends
+ * a pointer to a cleared device int that a failed assert sets; `shared=`
+ * bytes of dynamic LDS; `coop=1` launches cooperatively. Before the first
+ * launch the count below is compared with what the arguments produce.
+ *
+ * How many of its own parameters (not the hidden ones the runtime appends)
+ * `kernel` declares in the gfx950 code object `image`, read from the code
+ * object's metadata; -1 when the image, its metadata or the kernel is
+ * absent. Replaces, for AMDGPU images, the reference's
+ * vx_launch_entry_param_count (runtime/vx_kernel_launch.h:206-222, PTX) and
+ * vx_launch_entry_param_count_spirv (:248-315). */
+int32_t vx_hip_image_param_count(const void *image, size_t image_size,
+                                 const char *kernel);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,7 @@ CTRL_VENDOR_BASE = 0x1000
 HIP_CTRL_GEMM_KERNEL = CTRL_VENDOR_BASE + 1
 HIP_CTRL_STATS = CTRL_VENDOR_BASE + 2
 HIP_CTRL_POOL_DRAIN = CTRL_VENDOR_BASE + 3
+HIP_CTRL_IMAGE_STATS = CTRL_VENDOR_BASE + 4
 (GEMM_AUTO, GEMM_MFMA, GEMM_TILED, GEMM_MFMA_PIPE4, GEMM_MFMA_PIPE8, GEMM_MFMA_IL, GEMM_MFMA_DMA,
  GEMM_MFMA_DMA8, GEMM_MFMA_PP) = (0, 1, 2, 3, 4, 5, 6, 7, 8)
 
@@ -76,6 +77,15 @@ def matmul_payload(name: str = "vx_npu_kernel_0", roles: str = "a:0,b:2,out:5",
     if topo is not None:
         entries["topo"] = str(topo)
     return payload(name, **entries)
+
+
+def image_payload(name: str, image: bytes, fmt: str = "hsaco", **entries: str) -> bytes:
+    """A payload whose device image rides in the binary section: the text
+    entries (``abi=1``, the given ones, ``format=``), the empty entry, the
+    image's length as a little-endian u64, then its bytes (the section
+    grammar of reference include/vx_hardware_runtime.h:414-563)."""
+    fields = {"abi": str(PAYLOAD_ABI), **entries, "format": fmt}
+    return payload(name, **fields) + b"\0" + len(image).to_bytes(8, "little") + image
 
 
 class Descriptor:
@@ -150,8 +160,11 @@ class CallArgs:
     tags: list[int] = field(default_factory=list)
     _cells: list = field(default_factory=list)
     _ptrs: list[int] = field(default_factory=list)
+    _launch_values: int = 0
 
     def memref(self, desc: Descriptor, dtype: int) -> "CallArgs":
+        if self._launch_values:
+            raise ValueError("launch values come after every kernel argument")
         cell = ctypes.c_void_p(desc.address)
         self._cells.append((cell, desc))
         self._ptrs.append(ctypes.addressof(cell))
@@ -162,13 +175,27 @@ class CallArgs:
         """A slot argument: `storage` is a SlotStorage, or a rank-0 slot
         memref naming an existing descriptor (a local tensor captured through
         its slot)."""
+        if self._launch_values:
+            raise ValueError("launch values come after every kernel argument")
         cell = ctypes.c_void_p(storage.address)
         self._cells.append((cell, storage))
         self._ptrs.append(ctypes.addressof(cell))
         self.tags.append(slot_tag(dtype, rank))
         return self
 
+    def launch_value(self, value: int) -> "CallArgs":
+        """An i32 launch value (`$j` of a payload's shape entries): placed after
+        the kernel's arguments and not counted in num_args."""
+        self._scalar(value, KIND_I32)
+        self._launch_values += 1
+        return self
+
     def scalar(self, value, kind: int) -> "CallArgs":
+        if self._launch_values:
+            raise ValueError("launch values come after every kernel argument")
+        return self._scalar(value, kind)
+
+    def _scalar(self, value, kind: int) -> "CallArgs":
         ctype = {KIND_I1: ctypes.c_uint8, KIND_I8: ctypes.c_int8, KIND_I16: ctypes.c_int16,
                  KIND_I32: ctypes.c_int32, KIND_I64: ctypes.c_int64, KIND_F32: ctypes.c_float,
                  KIND_F64: ctypes.c_double}[kind]
@@ -179,11 +206,13 @@ class CallArgs:
         return self
 
     def arrays(self):
+        """(device_args, arg_tags, num_args); launch values follow the
+        num_args kernel arguments in both arrays."""
         n = len(self._ptrs)
         args = (ctypes.c_void_p * max(n, 1))(*self._ptrs)
         tags = (ctypes.c_int32 * max(n, 1))(*[t if t < 2**31 else t - 2**32 for t in self.tags])
         self._cells.append((args, tags))
-        return args, tags, n
+        return args, tags, n - self._launch_values
 
 
 class SlotRef:

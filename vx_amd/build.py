@@ -99,6 +99,31 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+TEST_IMAGES = ROOT / "tests" / "images"
+
+
+def build_test_images(verbose: bool = False) -> list[Path]:
+    """Code objects for the payload-image tests: each tests/images/*.hip as a
+    bare gfx950 ELF (<name>.hsaco) and as a clang offload bundle
+    (<name>.bundle.hsaco). Contraction off, so each kernel's f32 arithmetic
+    rounds once per operation, as numpy does."""
+    out = []
+    for src in sorted(TEST_IMAGES.glob("*.hip")):
+        for bundle in (False, True):
+            dst = src.with_suffix(".bundle.hsaco" if bundle else ".hsaco")
+            cmd = [hipcc(), "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+                   "-ffp-contract=off",
+                   "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                   *([] if bundle else ["--no-gpu-bundle-output"]), str(src), "-o", str(dst)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            if res.returncode != 0:
+                raise RuntimeError(f"compiling {src.name} failed:\n{res.stderr}")
+            out.append(dst)
+    return out
+
+
 def build_oracle(verbose: bool = False) -> None:
     """The CPU checker (oracle/liboracle.so) and, where the reference checkout
     exists, oracle/_ref/libvx_x86_dispatch.so built from its sources."""
@@ -111,4 +136,5 @@ def build_oracle(verbose: bool = False) -> None:
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    build_test_images(verbose="-v" in sys.argv)
     build_oracle(verbose="-v" in sys.argv)

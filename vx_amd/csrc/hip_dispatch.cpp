@@ -13,9 +13,13 @@
  *    host loop nest is routed to the GPU too;
  *  - operands already in HBM are used in place; host operands are staged
  *    through an exact-size pool (vx_device_pool_hip.h);
+ *  - a region whose payload carries a gfx950 code object (`format=hsaco`,
+ *    the image in the payload's binary section) runs from that image, with
+ *    its parameters marshalled and counted against the image's metadata
+ *    (vx_image_launch.h; reference runtime/cuda_dispatch.cpp:1364-1675 does
+ *    the same for PTX);
  *  - everything else runs as the outlined host kernel, with HBM views copied
- *    out and back (vx_host_fallback.h), because the compiler emits no AMDGPU
- *    image yet;
+ *    out and back (vx_host_fallback.h);
  *  - flash attention and the int8 GEMV are library ops (include/vx_hip_ops.h).
  *
  * Streams: each thread launches on its caller stream (vx_cuda_set_stream;
@@ -32,12 +36,16 @@
 #include "vx_dispatch_plan.h"
 #include "vx_hip_common.h"
 #include "vx_host_fallback.h"
+#include "vx_image_launch.h"
 #include "vx_kernels.h"
 #include "vx_ops_internal.h"
+
+#include <dlfcn.h>
 
 #include <atomic>
 #include <cstring>
 #include <map>
+#include <string>
 #include <mutex>
 #include <tuple>
 
@@ -177,6 +185,8 @@ std::atomic<int64_t> stat_gemm_mfma{0};
 std::atomic<int64_t> stat_gemm_tiled{0};
 std::atomic<int64_t> stat_host_fallback{0};
 std::atomic<int64_t> stat_staged_bytes{0};
+std::atomic<int64_t> stat_image_launches{0};
+std::atomic<int64_t> stat_image_loads{0};
 std::atomic<int> forced_gemm_kernel{0};
 
 /* An operand on the device: used in place, or a pooled packed copy. */
@@ -334,6 +344,225 @@ vx::HostCopies host_copies() {
     VX_HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
   };
   return io;
+}
+
+/* The gfx name of the current device ("gfx950"), without feature flags. */
+std::string device_arch() {
+  int device = 0;
+  VX_HIP_CHECK(hipGetDevice(&device));
+  hipDeviceProp_t prop;
+  VX_HIP_CHECK(hipGetDeviceProperties(&prop, device));
+  std::string arch = prop.gcnArchName;
+  const size_t colon = arch.find(':');
+  return colon == std::string::npos ? arch : arch.substr(0, colon);
+}
+
+/* A loaded image's kernel. Keyed by kernel name, device, the library that
+ * holds the payload (two libraries may use one kernel name), the image's
+ * address and size, and a hash of its first and last 256 bytes (a payload
+ * built at run time may reuse an address for another image). */
+struct LoadedImage {
+  hipModule_t module = nullptr;
+  hipFunction_t fn = nullptr;
+  int declared = -1;
+};
+std::mutex images_mutex;
+std::map<std::string, LoadedImage> &images() {
+  static auto *m = new std::map<std::string, LoadedImage>();
+  return *m;
+}
+
+uint64_t image_edges_hash(const unsigned char *b, size_t n) {
+  uint64_t h = 1469598103934665603ull;
+  const size_t head = n < 256 ? n : 256;
+  for (size_t i = 0; i < head; ++i) {
+    h = (h ^ b[i]) * 1099511628211ull;
+  }
+  for (size_t i = n - head; i < n; ++i) {
+    h = (h ^ b[i]) * 1099511628211ull;
+  }
+  return h;
+}
+
+/* The flag an `assert_flag=1` kernel sets when an assert fails: one int per
+ * device, cleared before each such launch. */
+int *assert_flag(int device) {
+  static std::mutex m;
+  static std::map<int, int *> flags;
+  std::lock_guard<std::mutex> hold(m);
+  int *&f = flags[device];
+  if (!f) {
+    VX_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&f), sizeof(int)));
+  }
+  return f;
+}
+
+/* Run the code object the payload carries. False -- leaving the host
+ * fallback to run the region -- when the payload has no gfx950 image, or an
+ * argument cannot be marshalled or lives in host memory. A broken image, a
+ * parameter count that disagrees with the image, or a shape no GPU launches
+ * is fatal (reference runtime/cuda_dispatch.cpp:1364-1675,
+ * runtime/xpu_dispatch.cpp:470-705). */
+bool run_device_image(const void *payload, size_t payload_size,
+                      void **device_args, const int32_t *arg_tags,
+                      int64_t num_args) {
+  const char *name = static_cast<const char *>(payload);
+  const char *format = vx_payload_field(payload, payload_size, "format=");
+  if (!format || strcmp(format, "hsaco") != 0) {
+    if (format && verbose()) {
+      fprintf(stderr,
+              "[Vx HIP] %s has format=%s, which this library does not load\n",
+              name, format);
+    }
+    return false;
+  }
+  const void *image = nullptr;
+  const int64_t image_size = vx_payload_section(payload, payload_size, &image);
+  if (image_size <= 0 || !image) {
+    if (verbose()) {
+      fprintf(stderr,
+              "[Vx HIP] %s says format=hsaco but carries no usable image "
+              "section (code %lld)\n",
+              name, (long long)image_size);
+    }
+    return false;
+  }
+  select_device(vx_payload_topology(payload, payload_size), "image launch");
+  int device = 0;
+  VX_HIP_CHECK(hipGetDevice(&device));
+
+  const char *flag_field = vx_payload_field(payload, payload_size, "assert_flag=");
+  const bool takes_flag = flag_field && strcmp(flag_field, "1") == 0;
+  vx::ImageParams params;
+  if (!vx::image_build_params(device_args, arg_tags, num_args, params) ||
+      (takes_flag && params.count >= vx::kImageMaxParams)) {
+    if (verbose()) {
+      fprintf(stderr,
+              "[Vx HIP] %s has an argument this path cannot marshal (a "
+              "publication slot, or more than %d parameters); not "
+              "launching\n",
+              name, vx::kImageMaxParams);
+    }
+    return false;
+  }
+  for (int64_t i = 0; i < num_args; ++i) {
+    if (VX_ABI_KIND(arg_tags[i]) != VX_ABI_KIND_MEMREF) {
+      continue;
+    }
+    const void *desc = *static_cast<void *const *>(device_args[i]);
+    if (!is_device_ptr(vx_memref_aligned(desc))) {
+      if (verbose()) {
+        fprintf(stderr,
+                "[Vx HIP] %s: argument %lld is not in GPU memory; the host "
+                "runs it\n",
+                name, (long long)i);
+      }
+      return false;
+    }
+  }
+  Dl_info info;
+  const void *library = dladdr(payload, &info) ? info.dli_fbase : nullptr;
+  char key[512];
+  snprintf(key, sizeof key, "%s@%d@%p@%p@%lld@%016llx", name, device, library,
+           image, (long long)image_size,
+           (unsigned long long)image_edges_hash(
+               static_cast<const unsigned char *>(image), (size_t)image_size));
+  LoadedImage loaded;
+  {
+    std::lock_guard<std::mutex> hold(images_mutex);
+    auto found = images().find(key);
+    if (found != images().end()) {
+      loaded = found->second;
+    } else {
+      const std::string arch = device_arch();
+      loaded.declared = vx::code_object_param_count(
+          image, (size_t)image_size, arch.c_str(), name);
+      if (loaded.declared < 0) {
+        fprintf(stderr,
+                "[Vx HIP] FATAL: the image of %s holds no %s code object with "
+                "an entry %s whose parameters can be read\n",
+                name, arch.c_str(), name);
+        abort();
+      }
+      hipError_t e = hipModuleLoadData(&loaded.module, image);
+      if (e != hipSuccess) {
+        fprintf(stderr, "[Vx HIP] FATAL: the device image for %s did not load: %s\n",
+                name, hipGetErrorString(e));
+        abort();
+      }
+      e = hipModuleGetFunction(&loaded.fn, loaded.module, name);
+      if (e != hipSuccess) {
+        fprintf(stderr,
+                "[Vx HIP] FATAL: the device image loaded but has no entry "
+                "%s: %s\n",
+                name, hipGetErrorString(e));
+        abort();
+      }
+      images().emplace(key, loaded);
+      ++stat_image_loads;
+    }
+  }
+
+  const int given = params.count + (takes_flag ? 1 : 0);
+  if (loaded.declared != given) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: %s declares %d parameters and its arguments "
+            "produced %d.\n"
+            "          Launching would read past what was supplied.\n",
+            name, loaded.declared, given);
+    abort();
+  }
+  unsigned grid[3], block;
+  char why[160];
+  if (!vx::image_launch_geometry(payload, payload_size, device_args, arg_tags,
+                                 num_args, grid, &block, why, sizeof why)) {
+    fprintf(stderr, "[Vx HIP] FATAL: %s: %s\n", name, why);
+    abort();
+  }
+  int *flag = nullptr;
+  if (takes_flag) {
+    flag = assert_flag(device);
+    vxk::fill_i32_launch(flag, 0, caller_stream);
+    params.p[params.count] = &flag;
+  }
+  const char *shared_field = vx_payload_field(payload, payload_size, "shared=");
+  const unsigned shared =
+      shared_field ? (unsigned)strtoul(shared_field, nullptr, 10) : 0u;
+  const char *coop = vx_payload_field(payload, payload_size, "coop=");
+  hipError_t e;
+  if (coop && strcmp(coop, "0") != 0) {
+    /* Grid-wide barriers: every block must be resident at once, which the
+     * cooperative launch checks instead of letting the barrier wait forever. */
+    e = hipModuleLaunchCooperativeKernel(loaded.fn, grid[0], grid[1], grid[2],
+                                         block, 1, 1, shared, caller_stream,
+                                         params.p);
+  } else {
+    e = hipModuleLaunchKernel(loaded.fn, grid[0], grid[1], grid[2], block, 1,
+                              1, shared, caller_stream, params.p, nullptr);
+  }
+  if (e != hipSuccess) {
+    fprintf(stderr, "[Vx HIP] FATAL: launching %s failed: %s\n", name,
+            hipGetErrorString(e));
+    abort();
+  }
+  started_kernel(name);
+  ++stat_image_launches;
+  if (takes_flag) {
+    int failed = 0;
+    wait_for_kernels("an assert flag");
+    VX_HIP_CHECK(hipMemcpy(&failed, flag, sizeof failed, hipMemcpyDeviceToHost));
+    if (failed != 0) {
+      fprintf(stderr, "[Vx HIP] FATAL: an assert failed in %s\n", name);
+      abort();
+    }
+  }
+  if (verbose()) {
+    fprintf(stderr,
+            "[Vx HIP] %s ran on GPU %d from its own image (%d params, "
+            "%ux%ux%u blocks of %u)\n",
+            name, device, params.count, grid[0], grid[1], grid[2], block);
+  }
+  return true;
 }
 
 void run_on_host(const void *payload, size_t payload_size, void **device_args,
@@ -522,6 +751,10 @@ uint64_t vx_plugin_dispatch_async(const void *binary_payload,
       return 1;
     }
   }
+  if (hip_available() && run_device_image(binary_payload, payload_size,
+                                          device_args, arg_tags, num_args)) {
+    return 1;
+  }
   run_on_host(binary_payload, payload_size, device_args, arg_tags, num_args);
   return 1;
 }
@@ -664,10 +897,16 @@ void vx_plugin_arrivals_give(const void *site, void *count, size_t bytes,
 
 void vx_plugin_release_future(uint64_t future_id) { (void)future_id; }
 
+int32_t vx_hip_image_param_count(const void *image, size_t image_size,
+                                 const char *kernel) {
+  return vx::code_object_param_count(image, image_size, "gfx950", kernel);
+}
+
 /* Vendor opcodes of this library (VX_CTRL_VENDOR_BASE and up). */
 #define VX_HIP_CTRL_GEMM_KERNEL (VX_CTRL_VENDOR_BASE + 1)
 #define VX_HIP_CTRL_STATS (VX_CTRL_VENDOR_BASE + 2)
 #define VX_HIP_CTRL_POOL_DRAIN (VX_CTRL_VENDOR_BASE + 3)
+#define VX_HIP_CTRL_IMAGE_STATS (VX_CTRL_VENDOR_BASE + 4)
 
 int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   switch (opcode) {
@@ -748,6 +987,17 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     out[2] = stat_gemm_tiled.load();
     out[3] = stat_host_fallback.load();
     out[4] = stat_staged_bytes.load();
+    return 1;
+  }
+  case VX_HIP_CTRL_IMAGE_STATS: {
+    /* payload -> int64_t[2]: kernels launched from payload images, images
+     * loaded (one per kernel, device and image). */
+    int64_t *out = static_cast<int64_t *>(payload);
+    if (!out) {
+      return 0;
+    }
+    out[0] = stat_image_launches.load();
+    out[1] = stat_image_loads.load();
     return 1;
   }
   case VX_HIP_CTRL_POOL_DRAIN:

@@ -1448,4 +1448,13 @@ bool gemm_launch(const GemmArgs &g, hipStream_t stream) {
   return gemm_launch_kernel(gemm_pick(g), g, stream);
 }
 
+namespace {
+__global__ void fill_i32(int *p, int v) { *p = v; }
+} // namespace
+
+void fill_i32_launch(int *p, int v, hipStream_t stream) {
+  hipLaunchKernelGGL(fill_i32, dim3(1), dim3(1), 0, stream, p, v);
+  VX_HIP_CHECK(hipGetLastError());
+}
+
 } // namespace vxk

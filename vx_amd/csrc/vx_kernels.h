@@ -53,6 +53,10 @@ bool gemm_launch(const GemmArgs &g, hipStream_t stream);
 bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
                         hipStream_t stream);
 
+/* *p = v on `stream` (one thread; a kernel rather than hipMemsetAsync so a
+ * launch sequence stays capturable in a graph). */
+void fill_i32_launch(int *p, int v, hipStream_t stream);
+
 } // namespace vxk
 
 #endif /* VX_AMD_KERNELS_H */

@@ -72,6 +72,7 @@ HIP_SIGNATURES = {
     "vx_llama_i8_host_weights": (_vp, [_vp]),
     "vx_llama_i8_host_free": (None, [_vp]),
     "vx_llama_i8_save": (_i32, [ctypes.c_char_p, _vp, _vp]),
+    "vx_hip_image_param_count": (_i32, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]),
 }
 
 
@@ -114,6 +115,15 @@ class DispatchLibrary:
             raise RuntimeError("the library answered no statistics")
         return dict(gemm_device=out[0], gemm_mfma=out[1], gemm_tiled=out[2],
                     host_fallback=out[3], staged_bytes=out[4])
+
+    def image_stats(self) -> dict:
+        out = (ctypes.c_int64 * 2)()
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_IMAGE_STATS, out):
+            raise RuntimeError("the library answered no image statistics")
+        return dict(launches=out[0], loads=out[1])
+
+    def image_param_count(self, image: bytes, kernel: str) -> int:
+        return self.lib.vx_hip_image_param_count(image, len(image), kernel.encode())
 
     def force_gemm_kernel(self, which: int) -> None:
         v = ctypes.c_int32(which)
