@@ -289,16 +289,27 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
 }
 
 /* One workgroup per query head over positions 0..pos (reference
- * :275-325); scores in dynamic LDS. */
+ * :275-325); scores in dynamic LDS.
+ *
+ * Scores: kL lanes share a position, each taking kE consecutive elements of
+ * the head (hs = kE * kL), so a wave reads 64 / kL whole key rows with one
+ * coalesced load; a lane sums its kE products in order and the kL lanes add
+ * theirs by DPP. Values: lane i of each wave owns element i, the waves take
+ * positions round-robin, and each adds its positions in increasing order,
+ * eight loads in flight at a time; the four partial sums meet in LDS. */
+template <int kE, int kL>
 __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float score[];
   __shared__ float qs[256];
   __shared__ float part[kThreads];
   __shared__ float scratch[kThreads / 64];
+  constexpr int kPerWave = 64 / kL; /* positions one wave scores at a time */
   const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
   const int h = blockIdx.x;
-  const int hs = a.hs;
+  const int hs = kE * kL;
   const int hk = h / a.kv_mul;
   const int pos = *a.pos;
   const int n = pos + 1;
@@ -309,30 +320,73 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   const float *kb = a.kcache + hk * hs;
   const float *vb = a.vcache + hk * hs;
   const float root = sqrtf((float)hs);
-  float mx = -INFINITY;
-  for (int j = t; j < n; j += kThreads) {
-    const float *kr = kb + (int64_t)j * a.kv_dim;
-    float dot = 0.0f;
-    for (int i = 0; i < hs; ++i) {
-      dot = dot + qs[i] * kr[i];
-    }
-    const float s = dot / root;
-    score[j] = s;
-    mx = fmaxf(mx, s);
+  const int sub = lane % kL;  /* this lane's slice of the head */
+  const int slot = lane / kL; /* which of the wave's positions */
+  float qv[kE];
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    qv[e] = qs[sub * kE + e];
   }
-  mx = block_max(mx, scratch);
+  float mx = -INFINITY;
+  for (int j0 = wave * kPerWave; j0 < n; j0 += 4 * kPerWave) {
+    const int j = j0 + slot;
+    float kv[kE];
+    if (j < n) {
+      const float *kr = kb + (int64_t)j * a.kv_dim + sub * kE;
+      if constexpr (kE == 4) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(kr);
+        kv[0] = v4.x, kv[1] = v4.y, kv[2] = v4.z, kv[3] = v4.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < kE; ++e) {
+          kv[e] = kr[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kE; ++e) {
+        kv[e] = 0.0f;
+      }
+    }
+    float dot = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kE; ++e) {
+      dot = dot + qv[e] * kv[e];
+    }
+    dot = group_sum<kL>(dot);
+    if (j < n) {
+      const float sc = dot / root;
+      if (sub == 0) {
+        score[j] = sc;
+      }
+      mx = fmaxf(mx, sc);
+    }
+  }
+  mx = block_max(mx, scratch); /* also orders the score writes */
   float sum = 0.0f;
   for (int j = t; j < n; j += kThreads) {
     const float p = expf(score[j] - mx);
     score[j] = p;
     sum += p;
   }
-  sum = block_sum(sum, scratch); /* also orders the score writes */
+  sum = block_sum(sum, scratch); /* also orders the probability writes */
   const int groups = kThreads / hs;
   const int g = t / hs;
   const int i = t - g * hs;
   float acc = 0.0f;
-  for (int j = g; j < n; j += groups) {
+  int j = g;
+  for (; j + 7 * groups < n; j += 8 * groups) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      v[u] = vb[(int64_t)(j + u * groups) * a.kv_dim + i];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc = acc + score[j + u * groups] * v[u];
+    }
+  }
+  for (; j < n; j += groups) {
     acc = acc + score[j] * vb[(int64_t)j * a.kv_dim + i];
   }
   part[t] = acc;
@@ -448,8 +502,17 @@ void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
 
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
                            hipStream_t s) {
-  hipLaunchKernelGGL(step_attention, dim3(heads), dim3(kThreads),
-                     (size_t)seq_len * sizeof(float), s, a);
+  const size_t lds = (size_t)seq_len * sizeof(float);
+  switch (a.hs) {
+  case 2: hipLaunchKernelGGL((step_attention<2, 1>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 4: hipLaunchKernelGGL((step_attention<4, 1>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 8: hipLaunchKernelGGL((step_attention<4, 2>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 16: hipLaunchKernelGGL((step_attention<4, 4>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 32: hipLaunchKernelGGL((step_attention<4, 8>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 64: hipLaunchKernelGGL((step_attention<4, 16>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 128: hipLaunchKernelGGL((step_attention<4, 32>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  default: hipLaunchKernelGGL((step_attention<4, 64>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  }
 }
 
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s) {
