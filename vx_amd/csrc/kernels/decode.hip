@@ -146,58 +146,62 @@ __device__ __forceinline__ Best merge(Best a, Best b) {
 
 
 /* Classifier epilogue: the best and runner-up of this workgroup's rows
- * into part[blockIdx.x], for step_choose to merge. */
-__device__ void logits_best(const StepGemvArgs &a, float acc0, float acc1,
-                            bool live, int r0) {
+ * (each wave's lane 0 holds its own in `b`) into part[blockIdx.x], for
+ * step_choose to merge. */
+__device__ void logits_best(const StepGemvArgs &a, Best b) {
   __shared__ Best wbest[kThreads / 64];
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
   if (lane == 0) {
-    Best b{-INFINITY, 0x7fffffff, -INFINITY};
-    if (live) {
-      b = Best{a.scale[r0] * acc0, r0, -INFINITY};
-      b = merge(b, Best{a.scale[r0 + 1] * acc1, r0 + 1, -INFINITY});
-    }
     wbest[wave] = b;
   }
   __syncthreads();
   if (t == 0) {
-    Best b = wbest[0];
+    Best m = wbest[0];
     for (int w = 1; w < kThreads / 64; ++w) {
-      b = merge(b, wbest[w]);
+      m = merge(m, wbest[w]);
     }
-    a.part[blockIdx.x] = b;
+    a.part[blockIdx.x] = m;
   }
 }
 
 enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3 };
+
+/* Row pairs per wave: the classifier's waves take several, so its
+ * thousands of rows need fewer workgroups (one round over the CUs). */
+template <int kMode> constexpr int pairs_per_wave() { return kMode == 3 ? 4 : 1; }
 
 template <int kMode>
 __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
 #pragma clang fp contract(off)
   __shared__ float xin[kMaxCols];
   __shared__ float scratch[kThreads / 64];
+  constexpr int kPairs = pairs_per_wave<kMode>();
   const int t = threadIdx.x;
   const int cols = a.cols;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int r0 = (blockIdx.x * (kThreads / 64) + wave) * 2;
+  const int pair0 = (blockIdx.x * (kThreads / 64) + wave) * kPairs;
+  const int r0 = pair0 * 2; /* the first (for kPairs == 1, the only) pair */
   const bool live = r0 < a.rows;
 
   /* The weights do not depend on x: request them first, so their latency
    * runs under the normalisation below. */
   constexpr int kSegs = kMaxCols / 1024;
-  u32x4 wp[kSegs], wq[kSegs];
-  {
-    const int8_t *w0 = a.w + (int64_t)(live ? r0 : 0) * cols;
+  u32x4 wp[kPairs][kSegs], wq[kPairs][kSegs];
+#pragma unroll
+  for (int p = 0; p < kPairs; ++p) {
+    const int r = r0 + 2 * p;
+    const bool ok_r = r < a.rows;
+    const int8_t *w0 = a.w + (int64_t)(ok_r ? r : 0) * cols;
 #pragma unroll
     for (int s = 0; s < kSegs; ++s) {
       const int c = s * 1024 + lane * 16;
-      const bool ok = live && c < cols;
-      wp[s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + c) : u32x4{0, 0, 0, 0};
-      wq[s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + cols + c)
-                 : u32x4{0, 0, 0, 0};
+      const bool ok = ok_r && c < cols;
+      wp[p][s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + c) : u32x4{0, 0, 0, 0};
+      wq[p][s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + cols + c)
+                    : u32x4{0, 0, 0, 0};
     }
   }
 
@@ -206,43 +210,69 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       xin[i] = a.in[i];
     }
   } else {
-    /* RMSNorm as reference examples/llama.vx:145-158. */
+    /* RMSNorm as reference examples/llama.vx:145-158; x and the norm
+     * weights are read once, into registers, alongside the weights. */
+    constexpr int kPer = kMaxCols / kThreads;
+    float xv[kPer], nv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      xv[k] = i < cols ? a.x[i] : 0.0f;
+      nv[k] = i < cols ? a.norm[i] : 0.0f;
+    }
     float ss = 0.0f;
-    for (int i = t; i < cols; i += kThreads) {
-      const float v = a.x[i];
-      ss += v * v;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      if (t + k * kThreads < cols) {
+        ss += xv[k] * xv[k];
+      }
     }
     ss = block_sum(ss, scratch);
     const float inv = 1.0f / sqrtf(ss / (float)cols + 0.00001f);
-    for (int i = t; i < cols; i += kThreads) {
-      xin[i] = a.norm[i] * (inv * a.x[i]);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      if (i < cols) {
+        xin[i] = nv[k] * (inv * xv[k]);
+      }
     }
   }
   __syncthreads();
 
   float acc0 = 0.0f, acc1 = 0.0f;
+  Best best{-INFINITY, 0x7fffffff, -INFINITY};
 #pragma unroll
-  for (int s = 0; s < kSegs; ++s) {
-    const int c = s * 1024 + lane * 16;
-    if (c < cols) {
+  for (int p = 0; p < kPairs; ++p) {
+    acc0 = 0.0f;
+    acc1 = 0.0f;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const float xv = xin[c + k];
-        acc0 += (float)(int8_t)(wp[s][k >> 2] >> (8 * (k & 3))) * xv;
-        acc1 += (float)(int8_t)(wq[s][k >> 2] >> (8 * (k & 3))) * xv;
+    for (int s = 0; s < kSegs; ++s) {
+      const int c = s * 1024 + lane * 16;
+      if (c < cols) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const float xv = xin[c + k];
+          acc0 += (float)(int8_t)(wp[p][s][k >> 2] >> (8 * (k & 3))) * xv;
+          acc1 += (float)(int8_t)(wq[p][s][k >> 2] >> (8 * (k & 3))) * xv;
+        }
+      }
+    }
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    if constexpr (kMode == kLogits) {
+      const int r = r0 + 2 * p;
+      if (lane == 0 && r < a.rows) {
+        const float y0 = a.scale[r] * acc0;
+        const float y1 = a.scale[r + 1] * acc1;
+        a.out[r] = y0;
+        a.out[r + 1] = y1;
+        best = merge(best, Best{y0, r, -INFINITY});
+        best = merge(best, Best{y1, r + 1, -INFINITY});
       }
     }
   }
-  acc0 = wave_sum(acc0);
-  acc1 = wave_sum(acc1);
   if constexpr (kMode == kLogits) {
-    if (lane == 0 && live) {
-      const float y0 = a.scale[r0] * acc0;
-      const float y1 = a.scale[r0 + 1] * acc1;
-      a.out[r0] = y0;
-      a.out[r0 + 1] = y1;
-    }
-    logits_best(a, acc0, acc1, live, r0);
+    logits_best(a, best);
     return;
   }
   if (lane != 0 || !live) {
@@ -472,10 +502,15 @@ __global__ void step_start(StepArgmaxArgs a) {
   }
 }
 
+template <int kMode> int gemv_groups(int rows) {
+  constexpr int kPerGroup = (kThreads / 64) * pairs_per_wave<kMode>();
+  return (rows / 2 + kPerGroup - 1) / kPerGroup;
+}
+
 template <int kMode>
 void launch_gemv(const StepGemvArgs &a, hipStream_t s) {
-  const int groups = (a.rows / 2 + (kThreads / 64) - 1) / (kThreads / 64);
-  hipLaunchKernelGGL((step_gemv<kMode>), dim3(groups), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((step_gemv<kMode>), dim3(gemv_groups<kMode>(a.rows)),
+                     dim3(kThreads), 0, s, a);
 }
 
 } // namespace
@@ -490,9 +525,7 @@ void step_gemv_resid(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kResid>
 void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kSwiglu>(a, s); }
 void step_gemv_logits(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kLogits>(a, s); }
 
-int step_logits_groups(int rows) {
-  return (rows / 2 + (kThreads / 64) - 1) / (kThreads / 64);
-}
+int step_logits_groups(int rows) { return gemv_groups<kLogits>(rows); }
 
 void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
                         int nparts, hipStream_t s) {
