@@ -217,10 +217,17 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
   }
 }
 
+#ifndef VX_GEMV_U_SMALL
+#define VX_GEMV_U_SMALL 4 /* weight rows in flight per pass, batches <= 4 */
+#endif
+#ifndef VX_GEMV_U_BIG
+#define VX_GEMV_U_BIG 8 /* and for batches of 8 and 16 (measured best of 2, 4, 8) */
+#endif
+
 template <int kB>
 void launch_b(const int8_t *w, const float *s, const uint16_t *x, float *y,
               int rows, int cols, int nb, hipStream_t stream) {
-  constexpr int kU = kB <= 4 ? 4 : 2;
+  constexpr int kU = kB <= 4 ? VX_GEMV_U_SMALL : VX_GEMV_U_BIG;
   /* A workgroup loads its slice of x once per column group and reuses it for
    * all of its rows, so bigger batches take more rows per workgroup (x
    * traffic 2*kB/rows times the weights) at the cost of fewer workgroups;
