@@ -289,6 +289,57 @@ def test_mfma_pp_against_oracle(hiplib, k, out_dt, rng):
         assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-3)
 
 
+@pytest.mark.parametrize("m,n,k,ldb", [(1000, 776, 512, 776), (300, 4104, 64, 4104),
+                                       (257, 776, 96, 784), (1, 8, 32, 8), (4100, 296, 128, 304)])
+@pytest.mark.parametrize("out_dt", [abi.DTYPE_F32, abi.DTYPE_BF16])
+def test_mfma_pp_ragged_edges(hiplib, m, n, k, ldb, out_dt, rng):
+    """M and N that are not multiples of the 256x256 tile, and a B whose rows
+    are padded (ldb > n): edge tiles read zeros past the operands' ends and
+    store only inside C, which is checked to be untouched around the result."""
+    announce(f"gemm ping-pong ragged {m}x{n}x{k} ldb={ldb} out={out_dt}")
+    a16 = f32_to_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+    bpad = f32_to_bf16(rng.normal(0, 1, (k, ldb)).astype(np.float32))
+    b16 = np.ascontiguousarray(bpad[:, :n])
+    da, db = DeviceArray.of(hiplib, a16, abi.DTYPE_BF16), DeviceArray.of(hiplib, bpad, abi.DTYPE_BF16)
+    npt = np.float32 if out_dt == abi.DTYPE_F32 else np.uint16
+    sentinel = np.full((m + 2, n + 3), 7, npt)  # C is rows 1..m, cols 1..n of this
+    dc = DeviceArray.of(hiplib, sentinel, out_dt)
+    hiplib.force_gemm_kernel(abi.GEMM_MFMA_PP)
+    before = hiplib.stats()
+    matmul(hiplib, da.descriptor(), abi.DTYPE_BF16,
+           db.descriptor(sizes=(k, n), strides=(ldb, 1)), abi.DTYPE_BF16,
+           dc.descriptor(sizes=(m, n), strides=(n + 3, 1), offset=n + 3 + 1), out_dt)
+    full = dc.numpy()
+    after = hiplib.stats()
+    hiplib.force_gemm_kernel(abi.GEMM_AUTO)
+    assert after["gemm_mfma"] == before["gemm_mfma"] + 1
+    c = full[1:m + 1, 1:n + 1]
+    rest = full.copy()
+    rest[1:m + 1, 1:n + 1] = 7
+    assert np.all(rest == 7)
+    want = oracle.gemm_bf16_f32(a16, b16)
+    if out_dt == abi.DTYPE_F32:
+        assert_max_abs(c, want, 1e-3 * max(1.0, float(np.abs(want).max())), "ragged vs oracle")
+    else:
+        got = bf16_to_f32(c)
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max())
+    for x in (da, db, dc):
+        x.free()
+
+
+def test_mfma_pp_declines_n_off_the_16_byte_grid(hiplib, rng):
+    """N = 777: B's last row would end inside a 16-byte load, which the
+    buffer range check zeroes whole, so the ping-pong kernel declines and the
+    exact-order kernel runs (bit-equal to the oracle)."""
+    announce("gemm ping-pong declines n=777")
+    m, n, k = 257, 777, 96
+    a16 = f32_to_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1, (k, n)).astype(np.float32))
+    c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, abi.DTYPE_F32, kernel=abi.GEMM_MFMA_PP)
+    assert st["gemm_tiled"] == 1 and st["gemm_mfma"] == 0
+    assert np.array_equal(c, oracle.gemm_bf16_f32(a16, b16))
+
+
 def test_mfma_pp_f16(hiplib, rng):
     """f16 operands through the ping-pong kernel's f16 MFMA."""
     announce("gemm mfma ping-pong f16")

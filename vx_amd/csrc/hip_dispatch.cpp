@@ -272,9 +272,9 @@ bool run_gemm(const vx_gemm_plan &plan) {
 
   vxk::GemmKernel which = vxk::gemm_pick(g);
   const int forced = forced_gemm_kernel.load();
-  if (forced != 0 && (forced == vxk::GEMM_TILED || vxk::gemm_is_mfma(which))) {
-    /* A forced MFMA variant applies only where an MFMA kernel takes the
-     * shape; the tiled kernel takes every shape. */
+  if (forced != 0 && vxk::gemm_kernel_takes((vxk::GemmKernel)forced, g)) {
+    /* A forced kernel applies where it takes the shape; elsewhere the
+     * automatic choice stands. */
     which = (vxk::GemmKernel)forced;
   }
 

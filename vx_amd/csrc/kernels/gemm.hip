@@ -742,8 +742,8 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
 template <bool kBf16, int kOut>
 __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
+    void *__restrict__ C, int64_t M, int64_t N, int K, int64_t lda,
+    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n) {
   constexpr int kNS = 4;
   constexpr int kLoads = kDUnits / 64 / 8; /* per wave per plane */
   constexpr int kTM = 8;                   /* 16-row blocks per wave */
@@ -777,16 +777,23 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     const int bk = u >> 5;
     b_off[p] = (uint32_t)(bk * ldb * 2 + pswz_b(bk, u & 31) * 16);
   }
-  const int a_bytes = (int)((kTileM - 1) * lda * 2 + kDStageK * 2);
-  const int b_bytes = (int)((kDStageK - 1) * ldb * 2 + kTileN * 2);
+  /* A stage's loads cover a 256 x 32 block of A and a 32 x 256 block of B;
+   * each buffer ends at the last element of its matrix, so rows of A past M
+   * and the tail of B's last row read zeros. Columns of B past N within
+   * earlier rows read whatever follows them, which only reaches outputs past
+   * N, and those are not stored. */
+  const int64_t a_full = (kTileM - 1) * lda * 2 + kDStageK * 2;
+  const int64_t b_full = (kDStageK - 1) * ldb * 2 + kTileN * 2;
+  const int64_t a_end = ((M - 1) * lda + K) * 2; /* bytes from A */
+  const int64_t b_end = ((int64_t)(K - 1) * ldb + N) * 2;
 
   const uint32_t ring_base =
       (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
   auto issue = [&](int step, int slot) {
-    const i32x4 ra =
-        buffer_rsrc(A + m0 * lda + (int64_t)step * kDStageK, a_bytes);
-    const i32x4 rb =
-        buffer_rsrc(B + (int64_t)step * kDStageK * ldb + n0, b_bytes);
+    const int64_t a0 = m0 * lda + (int64_t)step * kDStageK;
+    const int64_t b0 = (int64_t)step * kDStageK * ldb + n0;
+    const i32x4 ra = buffer_rsrc(A + a0, (int)min(a_full, a_end - a0 * 2));
+    const i32x4 rb = buffer_rsrc(B + b0, (int)min(b_full, b_end - b0 * 2));
     const uint32_t la = ring_base + (uint32_t)(slot * 2 * kDUnits * 16) +
                         (uint32_t)(wave * kLoads * 64 * 16);
 #pragma unroll
@@ -884,7 +891,9 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t row = m0 + wm * 128 + i * 16 + 4 * kc + r;
-        put<kOut>(C, row * ldc + col, acc[i][jj][r]);
+        if (row < M && col < N) {
+          put<kOut>(C, row * ldc + col, acc[i][jj][r]);
+        }
       }
     }
   }
@@ -1224,6 +1233,27 @@ bool dma_takes(const GemmArgs &g) {
          (kDStageK - 1) * g.ldb * 2 + kTileN * 2 <= INT32_MAX;
 }
 
+/* The ping-pong kernel takes any M and any N that is a multiple of 8: edge
+ * tiles read zeros past the operands' ends and store only inside C. K must
+ * be whole stages of 32, and rows must start on 16-byte boundaries for the
+ * buffer-to-LDS loads. (The buffer range check zeroes a whole 16-byte load
+ * that straddles the end of B, so B's last row must end on a 16-byte
+ * boundary: N a multiple of 8.) */
+bool pp_takes(const GemmArgs &g) {
+  const bool sixteen = g.in_dtype == VX_DTYPE_BF16 || g.in_dtype == VX_DTYPE_F16;
+  const bool out_ok = g.out_dtype == VX_DTYPE_F32 || g.out_dtype == g.in_dtype;
+  if (!sixteen || !out_ok || g.m <= 0 || g.n <= 0 || g.k <= 0 ||
+      g.k % kDStageK != 0 || g.k > INT32_MAX || g.n % 8 != 0 || g.lda % 8 != 0 ||
+      g.ldb % 8 != 0 || g.lda < g.k || g.ldb < g.n || g.ldc < g.n ||
+      !aligned16(g.a) || !aligned16(g.b)) {
+    return false;
+  }
+  const int64_t tiles = ((g.m + kTileM - 1) / kTileM) * ((g.n + kTileN - 1) / kTileN);
+  return tiles <= INT32_MAX &&
+         (kTileM - 1) * g.lda * 2 + kDStageK * 2 <= INT32_MAX &&
+         (kDStageK - 1) * g.ldb * 2 + kTileN * 2 <= INT32_MAX;
+}
+
 bool tiled_takes(const GemmArgs &g) {
   if (g.m <= 0 || g.n <= 0 || g.k <= 0 || g.lda < g.k || g.ldb < g.n ||
       g.ldc < g.n) {
@@ -1296,11 +1326,12 @@ void launch_dma(const GemmArgs &g, hipStream_t s) {
 
 template <bool kBf16, int kOut>
 void launch_pp(const GemmArgs &g, hipStream_t s) {
-  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
+  const int tiles_m = (int)((g.m + kTileM - 1) / kTileM);
+  const int tiles_n = (int)((g.n + kTileN - 1) / kTileN);
   hipLaunchKernelGGL((gemm_mfma_pp<kBf16, kOut>), dim3(tiles_m * tiles_n),
                      dim3(512), 0, s, static_cast<const uint16_t *>(g.a),
-                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
-                     g.ldb, g.ldc, tiles_m, tiles_n);
+                     static_cast<const uint16_t *>(g.b), g.c, g.m, g.n,
+                     (int)g.k, g.lda, g.ldb, g.ldc, tiles_m, tiles_n);
 }
 
 void launch_pp_any(const GemmArgs &g, hipStream_t s) {
@@ -1361,8 +1392,30 @@ void launch_tiled(const GemmArgs &g, hipStream_t s) {
 
 } // namespace
 
+bool gemm_kernel_takes(GemmKernel which, const GemmArgs &g) {
+  switch (which) {
+  case GEMM_MFMA_256:
+  case GEMM_MFMA_PIPE4:
+  case GEMM_MFMA_PIPE8:
+  case GEMM_MFMA_IL:
+    return mfma_takes(g);
+  case GEMM_MFMA_DMA:
+  case GEMM_MFMA_DMA8:
+    return dma_takes(g);
+  case GEMM_MFMA_PP:
+    return pp_takes(g);
+  case GEMM_TILED:
+    return tiled_takes(g);
+  default:
+    return false;
+  }
+}
+
 GemmKernel gemm_pick(const GemmArgs &g) {
-  if (dma_takes(g)) {
+  /* Small products stay on the exact-order kernel: a 256x256 tile of mostly
+   * padding costs more than it saves there. */
+  const bool big = g.m >= 64 && g.n >= 64 && (double)g.m * g.n * g.k >= 16777216.0;
+  if (big && pp_takes(g)) {
     return GEMM_MFMA_PP;
   }
   if (mfma_takes(g)) {
@@ -1411,7 +1464,7 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
     }
     launch_dma_any<2, 4>(g, stream);
   } else if (which == GEMM_MFMA_PP) {
-    if (!dma_takes(g)) {
+    if (!pp_takes(g)) {
       return false;
     }
     launch_pp_any(g, stream);

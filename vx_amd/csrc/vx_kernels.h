@@ -47,6 +47,8 @@ inline bool gemm_is_mfma(GemmKernel k) {
 }
 
 GemmKernel gemm_pick(const GemmArgs &g);
+/* Whether one specific kernel takes the arguments. */
+bool gemm_kernel_takes(GemmKernel which, const GemmArgs &g);
 /* Launch; false when no kernel takes the arguments. */
 bool gemm_launch(const GemmArgs &g, hipStream_t stream);
 /* Launch one specific kernel; false when it does not take the arguments. */
