@@ -352,6 +352,56 @@ def test_mfma_pp_f16(hiplib, rng):
     assert np.abs(c - exact).max() <= 1e-5 * np.abs(exact).max()
 
 
+def test_f32_mfma_routed_at_1024(hiplib, rng):
+    """f32 products of 2^30 multiply-adds and more go to the f32 MFMA
+    kernel, whose sums round once per two products instead of once per
+    product: held to the reference's 1e-4 rule against the oracle, closer to
+    the f64 product than 1e-5 of its largest entry, and deterministic."""
+    announce("gemm f32 mfma 1024^3")
+    a = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    b = rng.uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    c, st = gpu_gemm(hiplib, a, b, abi.DTYPE_F32, abi.DTYPE_F32)
+    assert st["gemm_mfma"] == 1 and st["gemm_tiled"] == 0
+    again, _ = gpu_gemm(hiplib, a, b, abi.DTYPE_F32, abi.DTYPE_F32)
+    assert np.array_equal(c, again)
+    assert_rel(c, oracle.gemm_f32(a, b), FP32_REL, "f32 mfma 1024^3")
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(c - exact).max() <= 1e-5 * np.abs(exact).max()
+
+
+@pytest.mark.parametrize("m,n,k,lda,ldb", [(1000, 777, 333, 333, 777), (129, 131, 17, 20, 132),
+                                           (1, 1, 1, 1, 1), (300, 260, 64, 64, 264),
+                                           (130, 4100, 48, 52, 4100)])
+def test_f32_mfma_ragged(hiplib, m, n, k, lda, ldb, rng):
+    """The f32 MFMA kernel forced onto shapes off its 128x128x16 grid, with
+    padded rows and row strides that are not multiples of four floats (the
+    scalar load path): zeros past the operands' ends, stores only inside C,
+    which sits in a sentinel-filled buffer."""
+    announce(f"gemm f32 mfma ragged {m}x{n}x{k} lda={lda} ldb={ldb}")
+    apad = rng.uniform(-1, 1, (m, lda)).astype(np.float32)
+    bpad = rng.uniform(-1, 1, (k, ldb)).astype(np.float32)
+    da, db = DeviceArray.of(hiplib, apad, abi.DTYPE_F32), DeviceArray.of(hiplib, bpad, abi.DTYPE_F32)
+    sentinel = np.full((m + 2, n + 3), 7, np.float32)  # C is rows 1..m, cols 1..n of this
+    dc = DeviceArray.of(hiplib, sentinel, abi.DTYPE_F32)
+    hiplib.force_gemm_kernel(abi.GEMM_F32_MFMA)
+    before = hiplib.stats()
+    matmul(hiplib, da.descriptor(sizes=(m, k), strides=(lda, 1)), abi.DTYPE_F32,
+           db.descriptor(sizes=(k, n), strides=(ldb, 1)), abi.DTYPE_F32,
+           dc.descriptor(sizes=(m, n), strides=(n + 3, 1), offset=n + 3 + 1), abi.DTYPE_F32)
+    full = dc.numpy()
+    after = hiplib.stats()
+    hiplib.force_gemm_kernel(abi.GEMM_AUTO)
+    assert after["gemm_mfma"] == before["gemm_mfma"] + 1
+    c = full[1:m + 1, 1:n + 1]
+    rest = full.copy()
+    rest[1:m + 1, 1:n + 1] = 7
+    assert np.all(rest == 7)
+    a, b = np.ascontiguousarray(apad[:, :k]), np.ascontiguousarray(bpad[:, :n])
+    assert_rel(c, oracle.gemm_f32(a, b), FP32_REL, "f32 mfma ragged")
+    for x in (da, db, dc):
+        x.free()
+
+
 def test_flat_matvec(hiplib, rng):
     """vx_plugin_dispatch_async_flat: xout[i] = sum_j w[i*n+j] x[j]."""
     announce("flat matvec")

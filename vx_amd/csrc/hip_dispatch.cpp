@@ -967,9 +967,9 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
      * pipelined on 4 waves, 4 MFMA pipelined on 8 waves, 5 MFMA with the
      * non-MFMA work interleaved, 6/7 MFMA with direct-to-LDS loads (4 or 8
      * waves), 8 the same loads with SIMD-sharing waves taking turns on
-     * 16x16x32 MFMAs. */
+     * 16x16x32 MFMAs, 9 f32 on f32 MFMAs. */
     const int32_t *which = static_cast<const int32_t *>(payload);
-    if (!which || *which < 0 || *which > 8) {
+    if (!which || *which < 0 || *which > 9) {
       return 0;
     }
     forced_gemm_kernel.store(*which);

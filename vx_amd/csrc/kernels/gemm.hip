@@ -25,6 +25,11 @@
  * (runtime/host_dispatch_common.h:65-79), and for bf16 -> f32 the same as
  * the outlined linalg.matmul (extend, f32 multiply, f32 add, k sequential;
  * src/codegen/flat/emit/tensor.rs:1600-1647).
+ *
+ * f32 products of 2^30 multiply-adds and more go to gemm_f32_mfma
+ * (v_mfma_f32_32x32x2_f32, 128x128 tiles), which is within the reference's
+ * 1e-4 rule of that loop but not bit-equal to it; smaller f32 products,
+ * BASELINE's 512^3 plumbing case among them, stay exact-order.
  */
 #include "../../../include/vx_hardware_runtime.h"
 #include "../vx_hip_common.h"
@@ -1116,6 +1121,137 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_mfma_il(
   }
 }
 
+/* f32 GEMM on v_mfma_f32_32x32x2_f32, for products large enough that the
+ * exact-order kernel's rate matters: 128x128 tiles, 4 waves of 64x64 (2x2
+ * accumulators of 32x32), K in stages of 16 through a double-buffered LDS
+ * ring, the next stage's loads in registers while the current one computes.
+ * A is stored transposed ([k][m]) so that both operands reach the MFMA as 32
+ * consecutive floats per half-wave; rows are padded by 32 floats so the two
+ * half-waves hit different banks. Edge tiles load zeros outside the
+ * operands and store only inside C. Products are exact in f32 and each MFMA
+ * step rounds its sums, so results agree with the exact-order loop to about
+ * 1e-6 relative, not bit for bit. */
+constexpr int kF32Tile = 128;
+constexpr int kF32Ks = 16;
+constexpr int kF32Pad = kF32Tile + 32;
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256, 2) void gemm_f32_mfma(
+    const float *__restrict__ A, const float *__restrict__ B,
+    float *__restrict__ C, int64_t M, int64_t N, int64_t K, int64_t lda,
+    int64_t ldb, int64_t ldc) {
+  __shared__ float As[2][kF32Ks][kF32Pad]; /* [k][m] */
+  __shared__ float Bs[2][kF32Ks][kF32Pad]; /* [k][n] */
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.y * kF32Tile;
+  const int64_t n0 = (int64_t)blockIdx.x * kF32Tile;
+  const bool vec_a = (lda & 3) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  const bool vec_b = (ldb & 3) == 0 && (reinterpret_cast<uintptr_t>(B) & 15) == 0;
+
+  /* Thread t loads A rows (t + 256e) / 4, k columns 4 ((t + 256e) % 4) ..+3,
+   * and B k-row (t + 256e) / 32, columns 4 ((t + 256e) % 32) ..+3. */
+  f32x4v ra[2], rb[2];
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int idx = t + 256 * e;
+      const int64_t gm = m0 + (idx >> 2), gk = k0 + 4 * (idx & 3);
+      if (vec_a && gm < M && gk + 3 < K) {
+        ra[e] = *reinterpret_cast<const f32x4v *>(A + gm * lda + gk);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          ra[e][q] = (gm < M && gk + q < K) ? A[gm * lda + gk + q] : 0.0f;
+        }
+      }
+      const int64_t hk = k0 + (idx >> 5), hn = n0 + 4 * (idx & 31);
+      if (vec_b && hk < K && hn + 3 < N) {
+        rb[e] = *reinterpret_cast<const f32x4v *>(B + hk * ldb + hn);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          rb[e][q] = (hk < K && hn + q < N) ? B[hk * ldb + hn + q] : 0.0f;
+        }
+      }
+    }
+  };
+  auto stash = [&](int s) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int idx = t + 256 * e;
+      const int am = idx >> 2, ak = 4 * (idx & 3);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        As[s][ak + q][am] = ra[e][q];
+      }
+      *reinterpret_cast<f32x4v *>(&Bs[s][idx >> 5][4 * (idx & 31)]) = rb[e];
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+      }
+    }
+  }
+  const int lr = lane & 31;
+  const int lk = lane >> 5;
+  const int64_t stages = (K + kF32Ks - 1) / kF32Ks;
+  load(0);
+  stash(0);
+  __syncthreads();
+  for (int64_t st = 0; st < stages; ++st) {
+    const int s = (int)(st & 1);
+    if (st + 1 < stages) {
+      load((st + 1) * kF32Ks);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kF32Ks; kk += 2) {
+      float a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = As[s][kk + lk][wm * 64 + i * 32 + lr];
+        b[i] = Bs[s][kk + lk][wn * 64 + i * 32 + lr];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (st + 1 < stages) {
+      stash(s ^ 1);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn * 64 + j * 32 + lr;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (row < M && col < N) {
+          C[row * ldc + col] = acc[i][j][r];
+        }
+      }
+    }
+  }
+}
+
 template <int kIn>
 __device__ __forceinline__ auto load_in(const void *p, int64_t at) {
   if constexpr (kIn == VX_DTYPE_F64) {
@@ -1252,6 +1388,22 @@ bool pp_takes(const GemmArgs &g) {
   return tiles <= INT32_MAX &&
          (kTileM - 1) * g.lda * 2 + kDStageK * 2 <= INT32_MAX &&
          (kDStageK - 1) * g.ldb * 2 + kTileN * 2 <= INT32_MAX;
+}
+
+bool f32_mfma_takes(const GemmArgs &g) {
+  return g.in_dtype == VX_DTYPE_F32 && g.out_dtype == VX_DTYPE_F32 && g.m > 0 &&
+         g.n > 0 && g.k > 0 && g.lda >= g.k && g.ldb >= g.n && g.ldc >= g.n &&
+         (g.m + kF32Tile - 1) / kF32Tile <= 65535 &&
+         (g.n + kF32Tile - 1) / kF32Tile <= INT32_MAX;
+}
+
+void launch_f32_mfma(const GemmArgs &g, hipStream_t s) {
+  dim3 grid((unsigned)((g.n + kF32Tile - 1) / kF32Tile),
+            (unsigned)((g.m + kF32Tile - 1) / kF32Tile));
+  hipLaunchKernelGGL(gemm_f32_mfma, grid, dim3(256), 0, s,
+                     static_cast<const float *>(g.a),
+                     static_cast<const float *>(g.b), static_cast<float *>(g.c),
+                     g.m, g.n, g.k, g.lda, g.ldb, g.ldc);
 }
 
 bool tiled_takes(const GemmArgs &g) {
@@ -1404,6 +1556,8 @@ bool gemm_kernel_takes(GemmKernel which, const GemmArgs &g) {
     return dma_takes(g);
   case GEMM_MFMA_PP:
     return pp_takes(g);
+  case GEMM_F32_MFMA:
+    return f32_mfma_takes(g);
   case GEMM_TILED:
     return tiled_takes(g);
   default:
@@ -1417,6 +1571,12 @@ GemmKernel gemm_pick(const GemmArgs &g) {
   const bool big = g.m >= 64 && g.n >= 64 && (double)g.m * g.n * g.k >= 16777216.0;
   if (big && pp_takes(g)) {
     return GEMM_MFMA_PP;
+  }
+  /* f32: the exact-order kernel (bit-equal to the reference's host loop)
+   * below 2^30 multiply-adds, the MFMA kernel above. */
+  if (g.m >= 128 && g.n >= 128 && (double)g.m * g.n * g.k >= 1073741824.0 &&
+      f32_mfma_takes(g)) {
+    return GEMM_F32_MFMA;
   }
   if (mfma_takes(g)) {
     return GEMM_MFMA_PIPE4;
@@ -1468,6 +1628,11 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
       return false;
     }
     launch_pp_any(g, stream);
+  } else if (which == GEMM_F32_MFMA) {
+    if (!f32_mfma_takes(g)) {
+      return false;
+    }
+    launch_f32_mfma(g, stream);
   } else if (which == GEMM_TILED) {
     if (!tiled_takes(g)) {
       return false;

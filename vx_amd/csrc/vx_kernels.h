@@ -38,12 +38,13 @@ enum GemmKernel {
   GEMM_MFMA_DMA = 6,   /* as 1, global -> LDS direct, 4-deep ring of K=32 */
   GEMM_MFMA_DMA8 = 7,  /* as 6, 8 waves (two per SIMD) */
   GEMM_MFMA_PP = 8,    /* as 7 on 16x16x32 MFMAs, SIMD-sharing waves alternate */
+  GEMM_F32_MFMA = 9,   /* f32 on 32x32x2 f32 MFMAs, 128x128 tiles */
 };
 
 inline bool gemm_is_mfma(GemmKernel k) {
   return k == GEMM_MFMA_256 || k == GEMM_MFMA_PIPE4 || k == GEMM_MFMA_PIPE8 ||
          k == GEMM_MFMA_IL || k == GEMM_MFMA_DMA ||
-         k == GEMM_MFMA_DMA8 || k == GEMM_MFMA_PP;
+         k == GEMM_MFMA_DMA8 || k == GEMM_MFMA_PP || k == GEMM_F32_MFMA;
 }
 
 GemmKernel gemm_pick(const GemmArgs &g);
