@@ -13,19 +13,22 @@ from vx_amd.runtime import DeviceArray, gemv_i8
 pytestmark = pytest.mark.gpu
 
 
-def run(lib, w, s, x16):
+def run(lib, w, s, x16, guard=0):
+    """y through the op; with `guard`, y sits in a buffer `guard` floats
+    longer whose tail must come back untouched."""
     rows, cols = w.shape
     batch = x16.shape[0]
     dw = DeviceArray.of(lib, w, abi.DTYPE_I8)
     ds = DeviceArray.of(lib, s, abi.DTYPE_F32)
     dx = DeviceArray.of(lib, x16, abi.DTYPE_BF16)
-    dy = DeviceArray(lib, (batch, rows), abi.DTYPE_F32)
+    dy = DeviceArray.of(lib, np.full(batch * rows + guard, 7, np.float32), abi.DTYPE_F32)
     rc = gemv_i8(lib, dw.ptr, ds.ptr, dx.ptr, dy.ptr, rows, cols, batch)
     assert rc == 0
-    y = dy.numpy()
+    full = dy.numpy()
     for a in (dw, ds, dx, dy):
         a.free()
-    return y
+    assert np.all(full[batch * rows:] == 7)
+    return full[:batch * rows].reshape(batch, rows)
 
 
 def inputs(rng, rows, cols, batch):
@@ -49,14 +52,19 @@ def test_llama7b_shapes(hiplib, shape, batch):
 
 
 @pytest.mark.parametrize("shape,batch", [((7, 16), 1), ((33, 48), 3), ((1000, 2064), 5),
-                                         ((64, 4096), 16), ((1, 32), 2), ((9, 3000 + 8), 7)])
+                                         ((64, 4096), 16), ((1, 32), 2), ((9, 3000 + 8), 7),
+                                         ((8200, 1040), 12), ((17, 4112), 1), ((100, 48), 6),
+                                         ((8195, 4096), 16), ((31, 4160), 4)])
 def test_ragged(hiplib, shape, batch, rng):
+    """Rows that leave the last 16- or 32-row block partial, columns that end
+    inside a 256-column tile and inside a 64-column step, both kernels and
+    both tile heights; nothing is written past y."""
     announce(f"gemv ragged {shape} batch {batch}")
     rows, cols = shape
     if cols % 16:
         cols += 16 - cols % 16
     w, s, x16 = inputs(rng, rows, cols, batch)
-    y = run(hiplib, w, s, x16)
+    y = run(hiplib, w, s, x16, guard=64)
     assert_rel(y, oracle.gemv_i8_f64(w, s, x16), GEMV_REL, f"gemv {shape}")
 
 

@@ -1,5 +1,5 @@
 /*
- * gemv_i8.hip -- int8 weight-only GEMV / skinny GEMM, HBM-streaming, no MFMA.
+ * gemv_i8.hip -- int8 weight-only GEMV / skinny GEMM, HBM-streaming.
  *
  * y[b, r] = scale[r] * sum_c w[r, c] * x[b, c], w int8 [rows, cols], x bf16
  * [batch, cols], f32 sums.
@@ -8,8 +8,10 @@
  * non-temporal loads, in an order that sweeps W front to back across the
  * grid. The int8 weights become bf16 pairs exactly (|w| <= 127 fits bf16's
  * mantissa: a byte-to-f32 convert, then the high halves of two floats) and
- * meet x in v_dot2_f32_bf16, whose products are exact; every batch row
- * reuses one conversion.
+ * meet x either in v_dot2_f32_bf16 (gemv_i8_kernel: small batches over at
+ * most 4096 columns) or in v_mfma_f32_16x16x32_bf16 (gemv_i8_lds: the
+ * rest); the products are exact either way and every batch row reuses one
+ * conversion.
  */
 #include "../vx_hip_common.h"
 #include "../vx_ops_kernels.h"
@@ -217,6 +219,157 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
   }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma_bf16(const uint32_t *a, u32x4 b, f32x4 c) {
+  const u32x4 av = {a[0], a[1], a[2], a[3]};
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                 __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+/* MFMA GEMV with contiguous weight loads. Each wave owns a private LDS tile
+ * of 16 kR rows x kCols bytes: it loads the tile with 16-byte non-temporal
+ * buffer loads in which every wave instruction covers 1 KiB of W (1024 /
+ * kCols rows of kCols contiguous bytes: the shape that streams HBM best),
+ * writes it to the tile, and reads it back in the MFMA operand order (lane
+ * l: row l % 16 of each 16-row block, 16 bytes at column 16 (l / 16) of each
+ * 64-column step). Tile rows are padded by 16 bytes so those reads hit
+ * distinct banks. The tile is private to its wave, whose LDS operations
+ * complete in order, so only wave-scope ordering is needed between the
+ * writes and the reads.
+ *
+ * Loads retire in issue order, so each pass issues this tile's x loads,
+ * then writes the tile (waiting for its weights), then issues the next
+ * tile's weight loads, and only then waits for x: the prefetch stays in
+ * flight through the multiply. Buffer loads return zero past the end of
+ * their range, which covers the last rows, the last columns and the batch
+ * rows past nb without a branch.
+ *
+ * Workgroup g owns rows 16 kR g ..; its kW waves take the column tiles w,
+ * w + kW, ...; their accumulators meet in LDS at the end. */
+template <int kW, int kCols, int kR>
+__global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
+    const int8_t *__restrict__ W, const float *__restrict__ scale,
+    const uint16_t *__restrict__ X, float *__restrict__ Y, int rows, int cols,
+    int nb) {
+  constexpr int kRows = 16 * kR;
+  constexpr int kStride = kCols + 16;
+  constexpr int kLanesPerRow = kCols / 16;
+  constexpr int kRowsPerInst = 64 / kLanesPerRow;
+  constexpr int kInst = kRows / kRowsPerInst;
+  constexpr int kSteps = kCols / 64;
+  constexpr uint32_t kOut = 0x80000000u; /* past every range */
+  __shared__ __attribute__((aligned(16))) int8_t tile[kW][kRows * kStride];
+  __shared__ float red[kW][kRows][17];
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int m = lane & 15, g = lane >> 4;
+  const int r0 = (int)blockIdx.x * kRows;
+  const int lr = lane / kLanesPerRow;        /* row within an instruction */
+  const int lc = (lane % kLanesPerRow) * 16; /* byte column within the tile */
+  const int my_rows = min(kRows, rows - r0);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(W + (int64_t)r0 * cols), (short)0, my_rows * cols, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)X, (short)0, nb * cols * 2, 0x00020000);
+  int8_t *my = tile[wave];
+  const int ntiles = (cols + kCols - 1) / kCols;
+
+  u32x4 cur[kInst];
+  auto load_w = [&](int s) {
+    const int c = s * kCols + lc;
+#pragma unroll
+    for (int j = 0; j < kInst; ++j) {
+      const uint32_t off = c < cols ? (uint32_t)((j * kRowsPerInst + lr) * cols + c) : kOut;
+      cur[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, 2);
+    }
+  };
+  f32x4 acc[kR];
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+    acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  u32x4 xa[kSteps], xb[kSteps];
+  auto load_x = [&](int s) {
+#pragma unroll
+    for (int jj = 0; jj < kSteps; ++jj) {
+      const int c = s * kCols + 64 * jj + 8 * g;
+      const uint32_t off = (uint32_t)((m * cols + c) * 2);
+      xa[jj] = __builtin_amdgcn_raw_buffer_load_b128(
+          xr, (int)(m < nb && c < cols ? off : kOut), 0, 0);
+      xb[jj] = __builtin_amdgcn_raw_buffer_load_b128(
+          xr, (int)(m < nb && c + 32 < cols ? off + 64 : kOut), 0, 0);
+    }
+  };
+  int s = wave;
+  if (s < ntiles) {
+    load_w(s);
+  }
+  for (; s < ntiles; s += kW) {
+    load_x(s);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < kInst; ++j) {
+      *reinterpret_cast<u32x4 *>(my + (j * kRowsPerInst + lr) * kStride + lc) = cur[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + kW < ntiles) {
+      load_w(s + kW);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int jj = 0; jj < kSteps; ++jj) {
+#pragma unroll
+      for (int i = 0; i < kR; ++i) {
+        const int8_t *p = my + (16 * i + m) * kStride + 64 * jj + 8 * g;
+        const uint2 lo = *reinterpret_cast<const uint2 *>(p);
+        const uint2 hi = *reinterpret_cast<const uint2 *>(p + 32);
+        uint32_t wp[8];
+        bytes_to_bf16x2(u32x4{lo.x, lo.y, hi.x, hi.y}, wp);
+        acc[i] = mfma_bf16(wp, xa[jj], acc[i]);
+        acc[i] = mfma_bf16(wp + 4, xb[jj], acc[i]);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  /* Accumulator lane l holds batch row l % 16 of rows 4 (l / 16) + q. */
+#pragma unroll
+  for (int i = 0; i < kR; ++i) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      red[wave][16 * i + 4 * g + q][m] = acc[i][q];
+    }
+  }
+  __syncthreads();
+  for (int i = t; i < kRows * nb; i += kW * 64) {
+    const int rr = i % kRows, b = i / kRows;
+    if (rr < my_rows) {
+      float v = red[0][rr][b];
+#pragma unroll
+      for (int w = 1; w < kW; ++w) {
+        v += red[w][rr][b];
+      }
+      Y[(int64_t)b * rows + r0 + rr] = scale[r0 + rr] * v;
+    }
+  }
+}
+
+template <int kR>
+void launch_lds(const int8_t *w, const float *s, const uint16_t *x, float *y,
+                int rows, int cols, int nb, hipStream_t stream) {
+  const int grid = (rows + 16 * kR - 1) / (16 * kR);
+  hipLaunchKernelGGL((gemv_i8_lds<8, 256, kR>), dim3(grid), dim3(8 * 64), 0,
+                     stream, w, s, x, y, rows, cols, nb);
+}
+
 #ifndef VX_GEMV_U_SMALL
 #define VX_GEMV_U_SMALL 4 /* weight rows in flight per pass, batches <= 4 */
 #endif
@@ -251,7 +404,20 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
     return false;
   }
   const int r = (int)rows, c = (int)cols, nb = (int)batch;
-  if (nb == 1) {
+  /* The dot2 kernel holds each thread's columns of x in registers across all
+   * of its rows: the better choice while one pass of 4096 columns covers a
+   * row and the batch is small (its work per weight grows with the batch).
+   * Otherwise the MFMA kernel, whose cost beyond the weight stream is the x
+   * operand, read once per 16 (or, for big batches over many rows, 32) rows.
+   * Its buffer ranges (32 rows of W, all of x) take 31-bit byte counts. */
+  const bool mfma_ok = cols * 32 < INT32_MAX && cols * batch * 2 < INT32_MAX;
+  if (mfma_ok && (nb > 4 || c > kGroupCols)) {
+    if (nb >= 12 && r >= 8192) {
+      launch_lds<2>(w, scale, x, y, r, c, nb, stream);
+    } else {
+      launch_lds<1>(w, scale, x, y, r, c, nb, stream);
+    }
+  } else if (nb == 1) {
     launch_b<1>(w, scale, x, y, r, c, nb, stream);
   } else if (nb == 2) {
     launch_b<2>(w, scale, x, y, r, c, nb, stream);
