@@ -269,41 +269,71 @@ def bench_fa(lib, timer, steps: int, warmup: int):
 
 
 def bench_gemv(lib, timer, steps: int, warmup: int):
+    """BASELINE config 5 through vx_nn_gemv_i8_bf16. Each shape rotates
+    through enough weight copies to exceed twice the 256 MB MALL, so every
+    call streams its weights from HBM. `us` is the per-call time of a
+    hipGraph replay of the calls (the kernels back to back, as in a captured
+    decode step); `us_eager` the per-call time of the same calls made one by
+    one from Python, which adds the host's launch cost where that is the
+    longer of the two."""
     from vx_amd import abi
     from vx_amd.abi import f32_to_bf16
     from vx_amd.runtime import DeviceArray, gemv_i8
 
     out = []
     rng = np.random.default_rng(11)
-    for rows, cols in ((4096, 4096), (11008, 4096), (4096, 11008)):
-        wbytes = rows * cols
-        copies = max(6, -(-512 * 2**20 // wbytes))  # > 2x the 256 MB MALL
-        w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
-        ws = [DeviceArray.of(lib, w, abi.DTYPE_I8) for _ in range(copies)]
-        sc = DeviceArray.of(lib, rng.uniform(0.001, 0.01, rows).astype(np.float32), abi.DTYPE_F32)
-        for batch in (1, 4, 16):
-            x = DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((batch, cols)).astype(np.float32)),
-                               abi.DTYPE_BF16)
-            y = DeviceArray(lib, (batch, rows), abi.DTYPE_F32)
-            n_calls = max(steps, copies)
-            for i in range(warmup):
-                gemv_i8(lib, ws[i % copies].ptr, sc.ptr, x.ptr, y.ptr, rows, cols, batch)
-            timer.sync()
-            e0, e1 = timer.event(), timer.event()
-            timer.record(e0)
-            for i in range(n_calls):
-                rc = gemv_i8(lib, ws[i % copies].ptr, sc.ptr, x.ptr, y.ptr, rows, cols, batch)
-                assert rc == 0
-            timer.record(e1)
-            ms = timer.elapsed_ms(e0, e1) / n_calls
-            nbytes = rows * cols + 4 * rows + 2 * batch * cols + 4 * batch * rows
-            gbs = nbytes / (ms * 1e-3) / 1e9
-            out.append(dict(shape=[rows, cols], batch=batch, us=ms * 1e3, gbs=gbs,
-                            frac_of_hbm=gbs / PEAK_HBM_GBS, rotated_copies=copies))
-            x.free()
-            y.free()
-        for a in ws + [sc]:
-            a.free()
+    stream = timer.stream_create()
+    lib.lib.vx_hip_set_stream(stream)
+    try:
+        for rows, cols in ((4096, 4096), (11008, 4096), (4096, 11008)):
+            wbytes = rows * cols
+            copies = max(6, -(-512 * 2**20 // wbytes))  # > 2x the 256 MB MALL
+            w = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+            ws = [DeviceArray.of(lib, w, abi.DTYPE_I8) for _ in range(copies)]
+            sc = DeviceArray.of(lib, rng.uniform(0.001, 0.01, rows).astype(np.float32),
+                                abi.DTYPE_F32)
+            for batch in (1, 4, 16):
+                x = DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((batch, cols))
+                                                    .astype(np.float32)), abi.DTYPE_BF16)
+                y = DeviceArray(lib, (batch, rows), abi.DTYPE_F32)
+                n_calls = max(steps, copies)
+
+                def calls():
+                    for i in range(n_calls):
+                        rc = gemv_i8(lib, ws[i % copies].ptr, sc.ptr, x.ptr, y.ptr, rows,
+                                     cols, batch)
+                        assert rc == 0
+
+                for i in range(warmup):
+                    gemv_i8(lib, ws[i % copies].ptr, sc.ptr, x.ptr, y.ptr, rows, cols, batch)
+                timer.sync()
+                e0, e1 = timer.event(), timer.event()
+                timer.record(e0, stream)
+                calls()
+                timer.record(e1, stream)
+                us_eager = timer.elapsed_ms(e0, e1) / n_calls * 1e3
+                graph = timer.capture(stream, calls)
+                timer.graph_launch(graph, stream)  # warm
+                reps = 4
+                timer.record(e0, stream)
+                for _ in range(reps):
+                    timer.graph_launch(graph, stream)
+                timer.record(e1, stream)
+                us = timer.elapsed_ms(e0, e1) / (reps * n_calls) * 1e3
+                timer.graph_destroy(graph)
+                nbytes = rows * cols + 4 * rows + 2 * batch * cols + 4 * batch * rows
+                gbs = nbytes / (us * 1e-6) / 1e9
+                out.append(dict(shape=[rows, cols], batch=batch, us=us, gbs=gbs,
+                                frac_of_hbm=gbs / PEAK_HBM_GBS, us_eager=us_eager,
+                                rotated_copies=copies))
+                x.free()
+                y.free()
+            for a in ws + [sc]:
+                a.free()
+    finally:
+        timer.sync()
+        lib.lib.vx_hip_set_stream(None)
+        timer.stream_destroy(stream)
     return out
 
 

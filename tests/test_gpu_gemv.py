@@ -54,11 +54,14 @@ def test_llama7b_shapes(hiplib, shape, batch):
 @pytest.mark.parametrize("shape,batch", [((7, 16), 1), ((33, 48), 3), ((1000, 2064), 5),
                                          ((64, 4096), 16), ((1, 32), 2), ((9, 3000 + 8), 7),
                                          ((8200, 1040), 12), ((17, 4112), 1), ((100, 48), 6),
-                                         ((8195, 4096), 16), ((31, 4160), 4)])
+                                         ((8195, 4096), 16), ((31, 4160), 4),
+                                         ((4099, 4096), 2), ((6, 4096), 3), ((5, 8208), 1),
+                                         ((13, 12304), 1), ((3, 20480), 1), ((7, 2064), 4)])
 def test_ragged(hiplib, shape, batch, rng):
-    """Rows that leave the last 16- or 32-row block partial, columns that end
-    inside a 256-column tile and inside a 64-column step, both kernels and
-    both tile heights; nothing is written past y."""
+    """Rows that leave the last 16- or 32-row block (or 4-row group) partial,
+    columns that end inside a 256-column tile, a 64-column step or a
+    4096-column pass, one, two, three and more passes per load group, every
+    kernel and tile height; nothing is written past y."""
     announce(f"gemv ragged {shape} batch {batch}")
     rows, cols = shape
     if cols % 16:

@@ -5,13 +5,12 @@
  * [batch, cols], f32 sums.
  *
  * The weights are the traffic: every byte of W is read once, with 16-byte
- * non-temporal loads, in an order that sweeps W front to back across the
- * grid. The int8 weights become bf16 pairs exactly (|w| <= 127 fits bf16's
- * mantissa: a byte-to-f32 convert, then the high halves of two floats) and
- * meet x either in v_dot2_f32_bf16 (gemv_i8_kernel: small batches over at
- * most 4096 columns) or in v_mfma_f32_16x16x32_bf16 (gemv_i8_lds: the
- * rest); the products are exact either way and every batch row reuses one
- * conversion.
+ * non-temporal loads. The int8 weights become bf16 pairs exactly (|w| <= 127
+ * fits bf16's mantissa: a byte-to-f32 convert, then the high halves of two
+ * floats) and meet x either in v_dot2_f32_bf16 (gemv_i8_rows: batch 1, and
+ * batches up to 4 over at most 4096 columns) or in v_mfma_f32_16x16x32_bf16
+ * (gemv_i8_lds: the rest); the products are exact either way and every
+ * batch row reuses one conversion.
  */
 #include "../vx_hip_common.h"
 #include "../vx_ops_kernels.h"
@@ -133,8 +132,8 @@ __device__ __forceinline__ int wave_reduce_scatter(float (&v)[kB], int lane) {
   return b;
 }
 
-/* y[b, r] for kB batch rows (nb of them real, the rest padding), kU
- * weight rows in flight per pass.
+/* y[b, r] for batches of 3 and 4 over at most 4096 columns: kB batch rows
+ * (nb of them real, the rest padding), kU weight rows in flight per pass.
  *
  * Workgroup g owns rows g, g + G, g + 2G, ... (G = gridDim.x), so at any
  * moment the whole grid reads a contiguous band of W. Thread t owns columns
@@ -216,6 +215,105 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
       v += red[k][b][w];
     }
     Y[(int64_t)b * rows + r] = scale[r] * v;
+  }
+}
+
+/* y[b, r] for kB batch rows (nb of them real, the rest zero padding).
+ *
+ * Workgroup g owns the kR consecutive rows kR g .. kR g + kR - 1: one
+ * contiguous stretch of W. It walks the columns in passes of 4096 (thread t
+ * takes columns 16 t .. 16 t + 15 of each pass), kP passes at a time, and
+ * issues every load of those kP passes -- its x columns for each batch row,
+ * then its 16 bytes of each of the kR rows -- before it waits for any: the
+ * workgroup is one burst of reads, and the hardware keeps the CU full by
+ * starting the next workgroup as one ends. Buffer loads return zeros past
+ * the workgroup's rows, past the last column and past batch row nb, so the
+ * ragged edges need no branch (a branch around a load would make the
+ * compiler wait for it before issuing the next). The kR * kB partial sums
+ * go through one wave reduce-scatter and meet across the 4 waves in LDS. */
+template <int kB, int kR, int kP>
+__global__ __launch_bounds__(kThreads) void gemv_i8_rows(
+    const int8_t *__restrict__ W, const float *__restrict__ scale,
+    const uint16_t *__restrict__ X, float *__restrict__ Y, int rows, int cols,
+    int nb) {
+  constexpr int kV = kR * kB;
+  constexpr int kLog = log2i(kV);
+  static_assert((1 << kLog) == kV && kV <= 64, "kR * kB: a power of two");
+  constexpr uint32_t kOut = 0x80000000u; /* past every range */
+  __shared__ float red[kWaves][kV];
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int r0 = (int)blockIdx.x * kR;
+  const int my_rows = min(kR, rows - r0);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(W + (int64_t)r0 * cols), (short)0, my_rows * cols, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)X, (short)0, nb * cols * 2, 0x00020000);
+  float v[kV];
+#pragma unroll
+  for (int i = 0; i < kV; ++i) {
+    v[i] = 0.0f;
+  }
+  for (int c0 = 0; c0 < cols; c0 += kGroupCols * kP) {
+    u32x4 xl[kP][kB], xh[kP][kB], wv[kP][kR];
+#pragma unroll
+    for (int p = 0; p < kP; ++p) {
+      const int c = c0 + p * kGroupCols + t * 16;
+#pragma unroll
+      for (int b = 0; b < kB; ++b) {
+        const uint32_t off = c < cols ? (uint32_t)((b * cols + c) * 2) : kOut;
+        xl[p][b] = __builtin_amdgcn_raw_buffer_load_b128(xr, (int)off, 0, 0);
+        xh[p][b] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (int)(c < cols ? off + 16 : kOut), 0, 0);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kP; ++p) {
+      const int c = c0 + p * kGroupCols + t * 16;
+#pragma unroll
+      for (int u = 0; u < kR; ++u) {
+        const uint32_t off = c < cols ? (uint32_t)(u * cols + c) : kOut;
+        wv[p][u] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, 2);
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kP; ++p) {
+#pragma unroll
+      for (int u = 0; u < kR; ++u) {
+        uint32_t wp[8];
+        bytes_to_bf16x2(wv[p][u], wp);
+#pragma unroll
+        for (int b = 0; b < kB; ++b) {
+          float a = v[u * kB + b];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a = dot2(wp[q], xl[p][b][q], a);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            a = dot2(wp[4 + q], xh[p][b][q], a);
+          }
+          v[u * kB + b] = a;
+        }
+      }
+    }
+  }
+  const int i = wave_reduce_scatter<kV>(v, lane);
+  if ((lane & ((64 >> kLog) - 1)) == 0) {
+    red[wave][i] = v[0];
+  }
+  __syncthreads();
+  if (t < kV) {
+    const int u = t / kB, b = t % kB;
+    if (u < my_rows && b < nb) {
+      float sum = red[0][t];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) {
+        sum += red[w][t];
+      }
+      Y[(int64_t)b * rows + r0 + u] = scale[r0 + u] * sum;
+    }
   }
 }
 
@@ -370,26 +468,34 @@ void launch_lds(const int8_t *w, const float *s, const uint16_t *x, float *y,
                      stream, w, s, x, y, rows, cols, nb);
 }
 
-#ifndef VX_GEMV_U_SMALL
-#define VX_GEMV_U_SMALL 4 /* weight rows in flight per pass, batches <= 4 */
-#endif
-#ifndef VX_GEMV_U_BIG
-#define VX_GEMV_U_BIG 8 /* and for batches of 8 and 16 (measured best of 2, 4, 8) */
-#endif
-
-template <int kB>
-void launch_b(const int8_t *w, const float *s, const uint16_t *x, float *y,
-              int rows, int cols, int nb, hipStream_t stream) {
-  constexpr int kU = kB <= 4 ? VX_GEMV_U_SMALL : VX_GEMV_U_BIG;
-  /* A workgroup loads its slice of x once per column group and reuses it for
-   * all of its rows, so bigger batches take more rows per workgroup (x
-   * traffic 2*kB/rows times the weights) at the cost of fewer workgroups;
-   * never more than kMaxRows rows per workgroup. */
-  constexpr int kTarget = kB <= 2 ? 4 : kB <= 4 ? 8 : 16;
-  int grid = std::min(kMaxGrid, (rows + kTarget - 1) / kTarget);
+/* Batches of 3 and 4: 8 rows per workgroup, 4 in flight per thread. A
+ * workgroup loads its slice of x once and reuses it for all of its rows. */
+void launch_b4(const int8_t *w, const float *s, const uint16_t *x, float *y,
+               int rows, int cols, int nb, hipStream_t stream) {
+  int grid = std::min(kMaxGrid, (rows + 7) / 8);
   grid = std::max(grid, (rows + kMaxRows - 1) / kMaxRows);
-  hipLaunchKernelGGL((gemv_i8_kernel<kB, kU>), dim3(grid), dim3(kThreads), 0,
+  hipLaunchKernelGGL((gemv_i8_kernel<4, 4>), dim3(grid), dim3(kThreads), 0,
                      stream, w, s, x, y, rows, cols, nb);
+}
+
+/* gemv_i8_rows with kR rows per workgroup; one load group covers up to three
+ * 4096-column passes. Measured best: 4 rows for batch 1 (against 1, 2, 8 and
+ * 16) and 16 for batch 2 (against 4 and 8): x costs the workgroup 2 * kB
+ * bytes per column, the weights kR. */
+template <int kB, int kR>
+void launch_rows(const int8_t *w, const float *s, const uint16_t *x, float *y,
+                 int rows, int cols, int nb, hipStream_t stream) {
+  const dim3 grid((unsigned)((rows + kR - 1) / kR));
+  if (cols <= kGroupCols) {
+    hipLaunchKernelGGL((gemv_i8_rows<kB, kR, 1>), grid, dim3(kThreads), 0,
+                       stream, w, s, x, y, rows, cols, nb);
+  } else if (cols <= 2 * kGroupCols) {
+    hipLaunchKernelGGL((gemv_i8_rows<kB, kR, 2>), grid, dim3(kThreads), 0,
+                       stream, w, s, x, y, rows, cols, nb);
+  } else {
+    hipLaunchKernelGGL((gemv_i8_rows<kB, kR, 3>), grid, dim3(kThreads), 0,
+                       stream, w, s, x, y, rows, cols, nb);
+  }
 }
 
 } // namespace
@@ -397,36 +503,32 @@ void launch_b(const int8_t *w, const float *s, const uint16_t *x, float *y,
 bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
                     float *y, int64_t rows, int64_t cols, int64_t batch,
                     hipStream_t stream) {
+  /* Buffer ranges are 31-bit byte counts: 32 rows of W and all of x. */
   if (rows <= 0 || cols <= 0 || cols % 16 != 0 || rows > INT32_MAX ||
-      cols > INT32_MAX || batch < 1 || batch > 16 ||
+      cols > kGemvMaxCols || batch < 1 || batch > 16 ||
       (reinterpret_cast<uintptr_t>(w) & 15) ||
       (reinterpret_cast<uintptr_t>(x) & 15)) {
     return false;
   }
   const int r = (int)rows, c = (int)cols, nb = (int)batch;
-  /* The dot2 kernel holds each thread's columns of x in registers across all
-   * of its rows: the better choice while one pass of 4096 columns covers a
-   * row and the batch is small (its work per weight grows with the batch).
-   * Otherwise the MFMA kernel, whose cost beyond the weight stream is the x
-   * operand, read once per 16 (or, for big batches over many rows, 32) rows.
-   * Its buffer ranges (32 rows of W, all of x) take 31-bit byte counts. */
-  const bool mfma_ok = cols * 32 < INT32_MAX && cols * batch * 2 < INT32_MAX;
-  if (mfma_ok && (nb > 4 || c > kGroupCols)) {
-    if (nb >= 12 && r >= 8192) {
-      launch_lds<2>(w, scale, x, y, r, c, nb, stream);
-    } else {
-      launch_lds<1>(w, scale, x, y, r, c, nb, stream);
-    }
-  } else if (nb == 1) {
-    launch_b<1>(w, scale, x, y, r, c, nb, stream);
-  } else if (nb == 2) {
-    launch_b<2>(w, scale, x, y, r, c, nb, stream);
-  } else if (nb <= 4) {
-    launch_b<4>(w, scale, x, y, r, c, nb, stream);
-  } else if (nb <= 8) {
-    launch_b<8>(w, scale, x, y, r, c, nb, stream);
+  /* Routing, measured on 4096 x 4096, 11008 x 4096 and 4096 x 11008 with
+   * every kernel: gemv_i8_rows (dot2; each workgroup one burst of loads) for
+   * batch 1 at any width and batch 2 over at most 4096 columns; the
+   * grid-stride dot2 kernel, whose work per weight byte grows with the batch
+   * but overlaps the stream, for batches 3 and 4 over at most 4096 columns;
+   * otherwise the MFMA kernel, whose cost beyond the weight stream is the x
+   * operand, read once per 16 (or, for big batches over many rows, 32)
+   * rows. */
+  if (nb == 1) {
+    launch_rows<1, 4>(w, scale, x, y, r, c, nb, stream);
+  } else if (nb == 2 && c <= kGroupCols) {
+    launch_rows<2, 16>(w, scale, x, y, r, c, nb, stream);
+  } else if (nb <= 4 && c <= kGroupCols) {
+    launch_b4(w, scale, x, y, r, c, nb, stream);
+  } else if (nb >= 12 && r >= 8192) {
+    launch_lds<2>(w, scale, x, y, r, c, nb, stream);
   } else {
-    launch_b<16>(w, scale, x, y, r, c, nb, stream);
+    launch_lds<1>(w, scale, x, y, r, c, nb, stream);
   }
   VX_HIP_CHECK(hipGetLastError());
   return true;

@@ -12,8 +12,12 @@
 
 namespace vxk {
 
-/* y[b, r] = scale[r] * sum_c w[r, c] * x[b, c]; cols % 16 == 0, batch 1..16,
- * w and x 16-byte aligned. */
+/* Widest rows the GEMV kernels take: their buffer ranges (32 rows of w, all
+ * of x) are 31-bit byte counts. */
+constexpr int64_t kGemvMaxCols = int64_t(1) << 25;
+
+/* y[b, r] = scale[r] * sum_c w[r, c] * x[b, c]; cols % 16 == 0 and at most
+ * kGemvMaxCols, batch 1..16, w and x 16-byte aligned. */
 bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
                     float *y, int64_t rows, int64_t cols, int64_t batch,
                     hipStream_t stream);

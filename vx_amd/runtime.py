@@ -256,6 +256,45 @@ class HipTimer:
     def sync(self) -> None:
         self._check(self.hip.hipDeviceSynchronize(), "hipDeviceSynchronize")
 
+    def stream_create(self):
+        """A new stream at the default priority."""
+        self.hip.hipStreamCreate.argtypes = [ctypes.POINTER(_vp)]
+        s = _vp()
+        self._check(self.hip.hipStreamCreate(ctypes.byref(s)), "hipStreamCreate")
+        return s
+
+    def stream_destroy(self, s) -> None:
+        self.hip.hipStreamDestroy.argtypes = [_vp]
+        self._check(self.hip.hipStreamDestroy(s), "hipStreamDestroy")
+
+    def capture(self, stream, body):
+        """Run body() with `stream` capturing (relaxed mode), and return the
+        instantiated graph of what it launched there."""
+        h = self.hip
+        h.hipStreamBeginCapture.argtypes = [_vp, ctypes.c_int]
+        h.hipStreamEndCapture.argtypes = [_vp, ctypes.POINTER(_vp)]
+        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(_vp), _vp, _vp, _vp, ctypes.c_size_t]
+        h.hipGraphDestroy.argtypes = [_vp]
+        self._check(h.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")
+        try:
+            body()
+        finally:
+            g = _vp()
+            self._check(h.hipStreamEndCapture(stream, ctypes.byref(g)), "hipStreamEndCapture")
+        ex = _vp()
+        self._check(h.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0),
+                    "hipGraphInstantiate")
+        self._check(h.hipGraphDestroy(g), "hipGraphDestroy")
+        return ex
+
+    def graph_launch(self, ex, stream) -> None:
+        self.hip.hipGraphLaunch.argtypes = [_vp, _vp]
+        self._check(self.hip.hipGraphLaunch(ex, stream), "hipGraphLaunch")
+
+    def graph_destroy(self, ex) -> None:
+        self.hip.hipGraphExecDestroy.argtypes = [_vp]
+        self._check(self.hip.hipGraphExecDestroy(ex), "hipGraphExecDestroy")
+
     @staticmethod
     def _check(rc: int, what: str) -> None:
         if rc != 0:
