@@ -206,8 +206,22 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   }
 
   if constexpr (kMode == kResid) {
-    for (int i = t; i < cols; i += kThreads) {
-      xin[i] = a.in[i];
+    /* All of this thread's inputs in flight at once: a load-then-store
+     * loop would wait for each load in turn (and for the weights too, which
+     * were requested first). */
+    constexpr int kPer = kMaxCols / kThreads;
+    float iv[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      iv[k] = i < cols ? a.in[i] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      if (i < cols) {
+        xin[i] = iv[k];
+      }
     }
   } else {
     /* RMSNorm as reference examples/llama.vx:145-158; x and the norm
