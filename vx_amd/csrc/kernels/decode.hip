@@ -205,6 +205,8 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     }
   }
 
+  float fcr = 0.0f, fci = 0.0f;
+  int pos = 0;
   if constexpr (kMode == kResid) {
     /* All of this thread's inputs in flight at once: a load-then-store
      * loop would wait for each load in turn (and for the weights too, which
@@ -233,6 +235,19 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       const int i = t + k * kThreads;
       xv[k] = i < cols ? a.x[i] : 0.0f;
       nv[k] = i < cols ? a.norm[i] : 0.0f;
+    }
+    /* The rotary factors of this wave's (even, odd) pair depend only on the
+     * position: requested behind the weights and x, so that chain of two
+     * loads runs under them instead of after the GEMV. */
+    if constexpr (kMode == kQkv) {
+      pos = *a.pos;
+      if (live && r0 < a.dim + a.kv_dim) {
+        const int i = r0 < a.dim ? r0 : r0 - a.dim;
+        const int hd = i % a.hs;
+        const float *cs = a.rope + ((int64_t)pos * (a.hs / 2) + hd / 2) * 2;
+        fcr = cs[0];
+        fci = cs[1];
+      }
     }
     float ss = 0.0f;
 #pragma unroll
@@ -296,14 +311,10 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   const float y1 = a.scale[r0 + 1] * acc1;
 
   if constexpr (kMode == kQkv) {
-    const int pos = *a.pos;
-    const int dim = a.dim, kv_dim = a.kv_dim, hs = a.hs;
+    const int dim = a.dim, kv_dim = a.kv_dim;
     if (r0 < dim + kv_dim) {
       /* RoPE on the (even, odd) pair (reference :235-264). */
       const int i = r0 < dim ? r0 : r0 - dim;
-      const int hd = i % hs;
-      const float *cs = a.rope + ((int64_t)pos * (hs / 2) + hd / 2) * 2;
-      const float fcr = cs[0], fci = cs[1];
       const float e0 = y0 * fcr - y1 * fci;
       const float e1 = y0 * fci + y1 * fcr;
       if (r0 < dim) {
@@ -355,10 +366,12 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   const int h = blockIdx.x;
   const int hs = kE * kL;
   const int hk = h / a.kv_mul;
+  /* q does not depend on the position: both loads in flight together. */
+  const float qt = t < hs ? a.q[h * hs + t] : 0.0f;
   const int pos = *a.pos;
   const int n = pos + 1;
   if (t < hs) {
-    qs[t] = a.q[h * hs + t];
+    qs[t] = qt;
   }
   __syncthreads();
   const float *kb = a.kcache + hk * hs;
@@ -371,39 +384,50 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   for (int e = 0; e < kE; ++e) {
     qv[e] = qs[sub * kE + e];
   }
+  /* kChunk rows of keys per lane in flight at once (a wave covers
+   * kChunk * kPerWave positions per round trip to memory). */
+  constexpr int kChunk = 8;
+  constexpr int kStride = 4 * kPerWave; /* positions between a wave's rows */
   float mx = -INFINITY;
-  for (int j0 = wave * kPerWave; j0 < n; j0 += 4 * kPerWave) {
-    const int j = j0 + slot;
-    float kv[kE];
-    if (j < n) {
-      const float *kr = kb + (int64_t)j * a.kv_dim + sub * kE;
-      if constexpr (kE == 4) {
-        const float4 v4 = *reinterpret_cast<const float4 *>(kr);
-        kv[0] = v4.x, kv[1] = v4.y, kv[2] = v4.z, kv[3] = v4.w;
+  for (int j0 = wave * kPerWave; j0 < n; j0 += kStride * kChunk) {
+    float kv[kChunk][kE];
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int j = j0 + c * kStride + slot;
+      if (j < n) {
+        const float *kr = kb + (int64_t)j * a.kv_dim + sub * kE;
+        if constexpr (kE == 4) {
+          const float4 v4 = *reinterpret_cast<const float4 *>(kr);
+          kv[c][0] = v4.x, kv[c][1] = v4.y, kv[c][2] = v4.z, kv[c][3] = v4.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < kE; ++e) {
+            kv[c][e] = kr[e];
+          }
+        }
       } else {
 #pragma unroll
         for (int e = 0; e < kE; ++e) {
-          kv[e] = kr[e];
+          kv[c][e] = 0.0f;
         }
       }
-    } else {
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int j = j0 + c * kStride + slot;
+      float dot = 0.0f;
 #pragma unroll
       for (int e = 0; e < kE; ++e) {
-        kv[e] = 0.0f;
+        dot = dot + qv[e] * kv[c][e];
       }
-    }
-    float dot = 0.0f;
-#pragma unroll
-    for (int e = 0; e < kE; ++e) {
-      dot = dot + qv[e] * kv[e];
-    }
-    dot = group_sum<kL>(dot);
-    if (j < n) {
-      const float sc = dot / root;
-      if (sub == 0) {
-        score[j] = sc;
+      dot = group_sum<kL>(dot);
+      if (j < n) {
+        const float sc = dot / root;
+        if (sub == 0) {
+          score[j] = sc;
+        }
+        mx = fmaxf(mx, sc);
       }
-      mx = fmaxf(mx, sc);
     }
   }
   mx = block_max(mx, scratch); /* also orders the score writes */
