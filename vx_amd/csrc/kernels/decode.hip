@@ -205,6 +205,24 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     }
   }
 
+  /* The epilogue's operands (row scales; for the residual kernels the
+   * residual itself) do not depend on the GEMV either: requested now, so
+   * the epilogue does not wait a round trip for them. */
+  float sc0[kPairs], sc1[kPairs];
+#pragma unroll
+  for (int p = 0; p < kPairs; ++p) {
+    const int r = r0 + 2 * p;
+    sc0[p] = r < a.rows ? a.scale[r] : 0.0f;
+    sc1[p] = r < a.rows ? a.scale[r + 1] : 0.0f;
+  }
+  float res0 = 0.0f, res1 = 0.0f;
+  if constexpr (kMode == kResid) {
+    if (live) {
+      res0 = a.out[r0];
+      res1 = a.out[r0 + 1];
+    }
+  }
+
   float fcr = 0.0f, fci = 0.0f;
   int pos = 0;
   if constexpr (kMode == kResid) {
@@ -291,8 +309,8 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     if constexpr (kMode == kLogits) {
       const int r = r0 + 2 * p;
       if (lane == 0 && r < a.rows) {
-        const float y0 = a.scale[r] * acc0;
-        const float y1 = a.scale[r + 1] * acc1;
+        const float y0 = sc0[p] * acc0;
+        const float y1 = sc1[p] * acc1;
         a.out[r] = y0;
         a.out[r + 1] = y1;
         best = merge(best, Best{y0, r, -INFINITY});
@@ -307,8 +325,8 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   if (lane != 0 || !live) {
     return;
   }
-  const float y0 = a.scale[r0] * acc0;
-  const float y1 = a.scale[r0 + 1] * acc1;
+  const float y0 = sc0[0] * acc0;
+  const float y1 = sc1[0] * acc1;
 
   if constexpr (kMode == kQkv) {
     const int dim = a.dim, kv_dim = a.kv_dim;
@@ -330,8 +348,8 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       a.vcache[(int64_t)pos * kv_dim + i + 1] = y1;
     }
   } else if constexpr (kMode == kResid) {
-    a.out[r0] = a.out[r0] + y0;
-    a.out[r0 + 1] = a.out[r0 + 1] + y1;
+    a.out[r0] = res0 + y0;
+    a.out[r0 + 1] = res1 + y1;
   } else if constexpr (kMode == kSwiglu) {
     /* rows interleaved: 2i is W1 row i, 2i + 1 is W3 row i (reference
      * :377-384: val * (1 / (1 + exp(-val))) * h3). */
