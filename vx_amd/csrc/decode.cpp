@@ -7,8 +7,9 @@
  * cache) and W1/W3 interleaved row by row (one GEMV feeds SwiGLU). The
  * position and the next token live in device memory; a step is a fixed
  * sequence of 5 * layers + 2 launches that, with VX_LLAMA_GRAPH, is captured
- * once into a hipGraph and replayed per token with no host synchronisation
- * until the tokens are read back.
+ * once into a hipGraph (kept with the model while the prompt length and I/O
+ * buffers stay the same) and replayed per token with no host
+ * synchronisation until the tokens are read back.
  */
 #include "../../include/vx_hardware_runtime.h"
 #include "../../include/vx_hip_ops.h"
@@ -38,6 +39,11 @@ struct LlamaI8 {
   vxk::StepBest *best = nullptr; /* one per classifier workgroup */
   int prompt_cap = 0, out_cap = 0;
   hipStream_t stream = nullptr;
+  /* The instantiated step graph, kept across generate calls: it bakes in
+   * the prompt length and the I/O buffers, so it is dropped when either
+   * changes. */
+  hipGraphExec_t step_exec = nullptr;
+  int step_exec_prompt = -1;
   std::vector<void *> owned;
 };
 
@@ -55,7 +61,16 @@ template <typename T> T *alloc(LlamaI8 &m, size_t count) {
   return upload<T>(m, nullptr, count);
 }
 
+void drop_step_graph(LlamaI8 &m) {
+  if (m.step_exec) {
+    (void)hipGraphExecDestroy(m.step_exec);
+    m.step_exec = nullptr;
+  }
+  m.step_exec_prompt = -1;
+}
+
 void release(LlamaI8 &m) {
+  drop_step_graph(m);
   if (m.stream) {
     (void)hipStreamSynchronize(m.stream);
     (void)hipStreamDestroy(m.stream);
@@ -75,11 +90,13 @@ bool ensure_io(LlamaI8 &m, int n_prompt, int n_out) {
   if (n_prompt > m.prompt_cap) {
     m.prompt = alloc<int>(m, (size_t)n_prompt);
     m.prompt_cap = n_prompt;
+    drop_step_graph(m);
   }
   if (n_out > m.out_cap) {
     m.out_tokens = alloc<int>(m, (size_t)n_out);
     m.out_margin = alloc<float>(m, (size_t)n_out);
     m.out_cap = n_out;
+    drop_step_graph(m);
   }
   return true;
 }
@@ -307,18 +324,19 @@ int32_t vx_llama_i8_generate(void *model, const int32_t *prompt,
   vxk::step_start_launch(start, m->stream);
   const int positions = n_prompt + n_steps - 1;
   if (flags & VX_LLAMA_GRAPH) {
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
-    VX_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-    enqueue_step(*m, n_prompt);
-    VX_HIP_CHECK(hipStreamEndCapture(m->stream, &graph));
-    VX_HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
-    for (int p = 0; p < positions; ++p) {
-      VX_HIP_CHECK(hipGraphLaunch(exec, m->stream));
+    if (!m->step_exec || m->step_exec_prompt != n_prompt) {
+      drop_step_graph(*m);
+      hipGraph_t graph = nullptr;
+      VX_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+      enqueue_step(*m, n_prompt);
+      VX_HIP_CHECK(hipStreamEndCapture(m->stream, &graph));
+      VX_HIP_CHECK(hipGraphInstantiate(&m->step_exec, graph, nullptr, nullptr, 0));
+      VX_HIP_CHECK(hipGraphDestroy(graph));
+      m->step_exec_prompt = n_prompt;
     }
-    VX_HIP_CHECK(hipStreamSynchronize(m->stream));
-    VX_HIP_CHECK(hipGraphExecDestroy(exec));
-    VX_HIP_CHECK(hipGraphDestroy(graph));
+    for (int p = 0; p < positions; ++p) {
+      VX_HIP_CHECK(hipGraphLaunch(m->step_exec, m->stream));
+    }
   } else {
     for (int p = 0; p < positions; ++p) {
       enqueue_step(*m, n_prompt);

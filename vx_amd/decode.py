@@ -144,18 +144,24 @@ class LlamaI8:
 def bench(lib, timer, n_prompt: int = 16, n_steps: int = 256, reps: int = 3) -> dict:
     """dim 768 / 12 layers, int8, bs=1, 16-token prompt
     then 256 greedy tokens. Reports tokens per second of the whole generate
-    call (prompt positions included in the time) and the weight bytes each
-    position streams."""
+    call (prompt positions included in the time) with the step replayed as
+    a hipGraph (`tok_per_s`) and launched kernel by kernel
+    (`tok_per_s_eager`), and the weight bytes each position streams."""
     cfg = CONFIG_DECODE
     model = LlamaI8(lib, cfg, make_model(cfg, seed=0))
     prompt = make_prompt(cfg, n=n_prompt, seed=1)
-    model.generate(prompt, 8)  # warm: graph instantiation, first-touch
-    times = []
+    model.generate(prompt, n_steps)  # warm: graph instantiation, first-touch
+    model.generate(prompt, n_steps, graph=False)
+    times, eager = [], []
     toks = None
     for _ in range(reps):
         t0 = time.perf_counter()
         toks, margin = model.generate(prompt, n_steps)
         times.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        toks_e, _ = model.generate(prompt, n_steps, graph=False)
+        eager.append(time.perf_counter() - t0)
+        assert np.array_equal(toks, toks_e), "graph and eager steps disagree"
     model.close()
     best = min(times)
     positions = n_prompt + n_steps - 1
@@ -163,6 +169,7 @@ def bench(lib, timer, n_prompt: int = 16, n_steps: int = 256, reps: int = 3) -> 
     return dict(config="dim 768, 12 layers, int8 weights, bs=1, 16-token prompt + 256 greedy tokens",
                 tok_per_s=n_steps / best, positions_per_s=positions / best,
                 ms_per_position=best / positions * 1e3, runs_s=times,
+                tok_per_s_eager=n_steps / min(eager), runs_eager_s=eager,
                 weight_bytes_per_position=wbytes,
                 weight_gbs=wbytes * positions / best / 1e9,
                 first_tokens=[int(t) for t in toks[:8]])
