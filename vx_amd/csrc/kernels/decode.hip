@@ -172,10 +172,13 @@ enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3 };
  * thousands of rows need fewer workgroups (one round over the CUs). */
 template <int kMode> constexpr int pairs_per_wave() { return kMode == 3 ? 4 : 1; }
 
-template <int kMode>
+/* kSegs: 1024-column segments the kernel is built for (cols <= 1024 kSegs),
+ * so registers and LDS are sized to the matrix rather than to kMaxCols. */
+template <int kMode, int kSegs>
 __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
 #pragma clang fp contract(off)
-  __shared__ float xin[kMaxCols];
+  constexpr int kCols = kSegs * 1024;
+  __shared__ float xin[kCols];
   __shared__ float scratch[kThreads / 64];
   constexpr int kPairs = pairs_per_wave<kMode>();
   const int t = threadIdx.x;
@@ -188,7 +191,6 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
 
   /* The weights do not depend on x: request them first, so their latency
    * runs under the normalisation below. */
-  constexpr int kSegs = kMaxCols / 1024;
   u32x4 wp[kPairs][kSegs], wq[kPairs][kSegs];
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     /* All of this thread's inputs in flight at once: a load-then-store
      * loop would wait for each load in turn (and for the weights too, which
      * were requested first). */
-    constexpr int kPer = kMaxCols / kThreads;
+    constexpr int kPer = kCols / kThreads;
     float iv[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -246,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   } else {
     /* RMSNorm as reference examples/llama.vx:145-158; x and the norm
      * weights are read once, into registers, alongside the weights. */
-    constexpr int kPer = kMaxCols / kThreads;
+    constexpr int kPer = kCols / kThreads;
     float xv[kPer], nv[kPer];
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -565,8 +567,15 @@ template <int kMode> int gemv_groups(int rows) {
 
 template <int kMode>
 void launch_gemv(const StepGemvArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL((step_gemv<kMode>), dim3(gemv_groups<kMode>(a.rows)),
-                     dim3(kThreads), 0, s, a);
+  const dim3 grid(gemv_groups<kMode>(a.rows));
+  if (a.cols <= 1024) {
+    hipLaunchKernelGGL((step_gemv<kMode, 1>), grid, dim3(kThreads), 0, s, a);
+  } else if (a.cols <= 2048) {
+    hipLaunchKernelGGL((step_gemv<kMode, 2>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((step_gemv<kMode, kMaxCols / 1024>), grid, dim3(kThreads),
+                       0, s, a);
+  }
 }
 
 } // namespace
