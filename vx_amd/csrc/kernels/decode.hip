@@ -369,15 +369,17 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
  * Scores: kL lanes share a position, each taking kE consecutive elements of
  * the head (hs = kE * kL), so a wave reads 64 / kL whole key rows with one
  * coalesced load; a lane sums its kE products in order and the kL lanes add
- * theirs by DPP. Values: lane i of each wave owns element i, the waves take
- * positions round-robin, and each adds its positions in increasing order,
- * eight loads in flight at a time; the four partial sums meet in LDS. */
+ * theirs by DPP, eight key rows per lane in flight. Values: a lane owns
+ * four consecutive elements of the head (one float4; one element for heads
+ * under 16), the lane groups take positions round-robin, each adds its
+ * positions in increasing order with eight rows in flight, and the groups'
+ * partial sums meet in LDS. */
 template <int kE, int kL>
 __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float score[];
   __shared__ float qs[256];
-  __shared__ float part[kThreads];
+  __shared__ float part[kThreads * 4];
   __shared__ float scratch[kThreads / 64];
   constexpr int kPerWave = 64 / kL; /* positions one wave scores at a time */
   const int t = threadIdx.x;
@@ -458,31 +460,64 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
     sum += p;
   }
   sum = block_sum(sum, scratch); /* also orders the probability writes */
-  const int groups = kThreads / hs;
-  const int g = t / hs;
-  const int i = t - g * hs;
-  float acc = 0.0f;
+  /* Values: a lane takes kVec consecutive elements of a position's row
+   * (float4 where the head allows), so a wave reads whole rows; the lane
+   * groups take positions round-robin, each adding its positions in
+   * increasing order with eight rows in flight, and meet in LDS. */
+  constexpr int kHs = kE * kL;
+  constexpr int kVec = (kHs % 4 == 0 && kHs >= 16) ? 4 : 1;
+  constexpr int kRowLanes = kHs / kVec;
+  constexpr int kGroups = kThreads / kRowLanes;
+  const int g = t / kRowLanes;
+  const int i = (t - g * kRowLanes) * kVec;
+  float acc[kVec];
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) {
+    acc[e] = 0.0f;
+  }
+  auto row = [&](int jj, float (&v)[kVec]) {
+    const float *src = vb + (int64_t)jj * a.kv_dim + i;
+    if constexpr (kVec == 4) {
+      const float4 v4 = *reinterpret_cast<const float4 *>(src);
+      v[0] = v4.x, v[1] = v4.y, v[2] = v4.z, v[3] = v4.w;
+    } else {
+      v[0] = src[0];
+    }
+  };
   int j = g;
-  for (; j + 7 * groups < n; j += 8 * groups) {
-    float v[8];
+  for (; j + 7 * kGroups < n; j += 8 * kGroups) {
+    float v[8][kVec];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      v[u] = vb[(int64_t)(j + u * groups) * a.kv_dim + i];
+      row(j + u * kGroups, v[u]);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      acc = acc + score[j + u * groups] * v[u];
+      const float p = score[j + u * kGroups];
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        acc[e] = acc[e] + p * v[u][e];
+      }
     }
   }
-  for (; j < n; j += groups) {
-    acc = acc + score[j] * vb[(int64_t)j * a.kv_dim + i];
+  for (; j < n; j += kGroups) {
+    float v[kVec];
+    row(j, v);
+    const float p = score[j];
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) {
+      acc[e] = acc[e] + p * v[e];
+    }
   }
-  part[t] = acc;
+#pragma unroll
+  for (int e = 0; e < kVec; ++e) {
+    part[g * kHs + i + e] = acc[e];
+  }
   __syncthreads();
   if (t < hs) {
     float o = 0.0f;
-    for (int gg = 0; gg < groups; ++gg) {
-      o += part[gg * hs + t];
+    for (int gg = 0; gg < kGroups; ++gg) {
+      o += part[gg * kHs + t];
     }
     const float inv = 1.0f / sum;
     a.att[h * hs + t] = o * inv;
