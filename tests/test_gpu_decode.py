@@ -30,7 +30,14 @@ def assert_same_tokens(got, want, margin):
 
 @pytest.mark.parametrize("cfg", [CONFIG_TINY,
                                  LlamaConfig(dim=128, hidden_dim=256, n_layers=3, n_heads=2,
-                                             n_kv_heads=1, vocab_size=512, seq_len=96)])
+                                             n_kv_heads=1, vocab_size=512, seq_len=96),
+                                 # rows wider than 1024 and 2048 columns (the GEMVs built for
+                                 # 2 and 4 column segments), grouped KV heads
+                                 LlamaConfig(dim=1152, hidden_dim=3072, n_layers=1, n_heads=18,
+                                             n_kv_heads=6, vocab_size=512, seq_len=64),
+                                 # head size 128
+                                 LlamaConfig(dim=1024, hidden_dim=2816, n_layers=1, n_heads=8,
+                                             n_kv_heads=8, vocab_size=384, seq_len=48)])
 def test_logits_per_position_match_oracle(hiplib, cfg):
     announce(f"decode logits {cfg}")
     weights = make_model(cfg, seed=3)
