@@ -58,7 +58,7 @@ int32_t vx_nn_flash_attention_fwd_bf16(const uint16_t *q, const uint16_t *k,
  *
  * w: [rows, cols] int8 row-major; scale: [rows] f32; x: [batch, cols] bf16;
  * y: [batch, rows] f32. y[b, r] = scale[r] * sum_c w[r, c] * x[b, c], the sum
- * in f32. batch 1..16; cols a multiple of 16 and at most 2^25. */
+ * in f32. batch 1..16; cols a multiple of 16 and at most 2^24. */
 int32_t vx_nn_gemv_i8_bf16(const int8_t *w, const float *scale,
                            const uint16_t *x, float *y, int64_t rows,
                            int64_t cols, int64_t batch);

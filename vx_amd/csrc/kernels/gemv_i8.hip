@@ -359,8 +359,14 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
   constexpr int kInst = kRows / kRowsPerInst;
   constexpr int kSteps = kCols / 64;
   constexpr uint32_t kOut = 0x80000000u; /* past every range */
-  __shared__ __attribute__((aligned(16))) int8_t tile[kW][kRows * kStride];
-  __shared__ float red[kW][kRows][17];
+  /* The waves' tiles and, once every wave is past its last tile, the
+   * partial sums share one LDS block. */
+  constexpr int kTileBytes = kW * kRows * kStride;
+  constexpr int kRedBytes = kW * kRows * 17 * 4;
+  __shared__ __attribute__((aligned(16)))
+  int8_t smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
+  auto tile = reinterpret_cast<int8_t (*)[kRows * kStride]>(smem);
+  auto red = reinterpret_cast<float (*)[kRows][17]>(smem);
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -438,6 +444,7 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  __syncthreads(); /* every wave is done with its tile */
   /* Accumulator lane l holds batch row l % 16 of rows 4 (l / 16) + q. */
 #pragma unroll
   for (int i = 0; i < kR; ++i) {
@@ -503,7 +510,7 @@ void launch_rows(const int8_t *w, const float *s, const uint16_t *x, float *y,
 bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
                     float *y, int64_t rows, int64_t cols, int64_t batch,
                     hipStream_t stream) {
-  /* Buffer ranges are 31-bit byte counts: 32 rows of W and all of x. */
+  /* Buffer ranges are 31-bit byte counts: 64 rows of W and all of x. */
   if (rows <= 0 || cols <= 0 || cols % 16 != 0 || rows > INT32_MAX ||
       cols > kGemvMaxCols || batch < 1 || batch > 16 ||
       (reinterpret_cast<uintptr_t>(w) & 15) ||
@@ -517,16 +524,16 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
    * grid-stride dot2 kernel, whose work per weight byte grows with the batch
    * but overlaps the stream, for batches 3 and 4 over at most 4096 columns;
    * otherwise the MFMA kernel, whose cost beyond the weight stream is the x
-   * operand, read once per 16 (or, for big batches over many rows, 32)
-   * rows. */
+   * operand, read once per 16 (or, for batches of 8 and more over 8192 rows
+   * and more, 64) rows. */
   if (nb == 1) {
     launch_rows<1, 4>(w, scale, x, y, r, c, nb, stream);
   } else if (nb == 2 && c <= kGroupCols) {
     launch_rows<2, 16>(w, scale, x, y, r, c, nb, stream);
   } else if (nb <= 4 && c <= kGroupCols) {
     launch_b4(w, scale, x, y, r, c, nb, stream);
-  } else if (nb >= 12 && r >= 8192) {
-    launch_lds<2>(w, scale, x, y, r, c, nb, stream);
+  } else if (nb >= 8 && r >= 8192) {
+    launch_lds<4>(w, scale, x, y, r, c, nb, stream);
   } else {
     launch_lds<1>(w, scale, x, y, r, c, nb, stream);
   }

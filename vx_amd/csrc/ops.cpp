@@ -51,7 +51,7 @@ int32_t vx_nn_gemv_i8_bf16(const int8_t *w, const float *scale,
     return refuse(VX_OP_EUNSUPP, op, "cols must be a multiple of 16");
   }
   if (cols > vxk::kGemvMaxCols) {
-    return refuse(VX_OP_EUNSUPP, op, "cols must be at most 2^25");
+    return refuse(VX_OP_EUNSUPP, op, "cols must be at most 2^24");
   }
   if (!all_on_device({w, scale, x, y})) {
     return refuse(VX_OP_ENOTDEV, op, "every operand must be GPU memory");

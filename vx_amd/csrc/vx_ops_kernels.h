@@ -12,9 +12,9 @@
 
 namespace vxk {
 
-/* Widest rows the GEMV kernels take: their buffer ranges (32 rows of w, all
+/* Widest rows the GEMV kernels take: their buffer ranges (64 rows of w, all
  * of x) are 31-bit byte counts. */
-constexpr int64_t kGemvMaxCols = int64_t(1) << 25;
+constexpr int64_t kGemvMaxCols = int64_t(1) << 24;
 
 /* y[b, r] = scale[r] * sum_c w[r, c] * x[b, c]; cols % 16 == 0 and at most
  * kGemvMaxCols, batch 1..16, w and x 16-byte aligned. */
