@@ -152,6 +152,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     at.kv_dim = m.kv_dim;
     at.hs = m.hs;
     at.kv_mul = c.n_heads / c.n_kv_heads;
+    at.seq_len = c.seq_len;
     vxk::step_attention_launch(at, c.n_heads, c.seq_len, m.stream);
 
     vxk::StepGemvArgs wo = g;

@@ -388,52 +388,92 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   const int h = blockIdx.x;
   const int hs = kE * kL;
   const int hk = h / a.kv_mul;
-  /* q does not depend on the position: both loads in flight together. */
+  const int sub = lane % kL;  /* this lane's slice of the head */
+  const int slot = lane / kL; /* which of the wave's positions */
+  /* kChunk rows of keys per lane in flight at once (a wave covers
+   * kChunk * kPerWave positions per round trip to memory). */
+  constexpr int kChunk = 8;
+  constexpr int kStride = 4 * kPerWave; /* positions between a wave's rows */
+  /* The layer's caches as buffer ranges: a load past `bound` gets an
+   * offset past the range and returns zeros, so no branch surrounds a load
+   * (a branch would make the compiler wait for each load at the join). */
+  const int cache_bytes = a.seq_len * a.kv_dim * 4;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.kcache, (short)0, cache_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.vcache, (short)0, cache_bytes, 0x00020000);
+  constexpr uint32_t kOut = 0x80000000u; /* past every range */
+  auto key_rows = [&](int j0, int bound, float (&kv)[kChunk][kE]) {
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int j = j0 + c * kStride + slot;
+      const uint32_t off =
+          j < bound ? (uint32_t)((j * a.kv_dim + hk * hs + sub * kE) * 4) : kOut;
+      if constexpr (kE == 4) {
+        const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)off, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kv[c][e] = __uint_as_float(w[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < kE; ++e) {
+          kv[c][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+              krs, (int)(off == kOut ? kOut : off + 4 * e), 0, 0));
+        }
+      }
+    }
+  };
+  /* Values: a lane owns kVec consecutive elements of a position's row
+   * (float4 where the head allows), so a wave reads whole rows; the lane
+   * groups take positions round-robin. */
+  constexpr int kHs = kE * kL;
+  constexpr int kVec = (kHs % 4 == 0 && kHs >= 16) ? 4 : 1;
+  constexpr int kRowLanes = kHs / kVec;
+  constexpr int kGroups = kThreads / kRowLanes;
+  constexpr int kRows = 8; /* value rows per lane in flight */
+  const int g = t / kRowLanes;
+  const int i = (t - g * kRowLanes) * kVec;
+  /* Row jj of this lane's values, zeros from jj >= bound. */
+  auto row = [&](int jj, int bound, float (&v)[kVec]) {
+    const uint32_t off =
+        jj < bound ? (uint32_t)((jj * a.kv_dim + hk * hs + i) * 4) : kOut;
+    if constexpr (kVec == 4) {
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)off, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = __uint_as_float(w[e]);
+      }
+    } else {
+      v[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(vrs, (int)off, 0, 0));
+    }
+  };
+
+  /* q, the first chunk of key rows and the first value rows do not depend
+   * on the position: they are requested together with it, bounded by the
+   * cache's length rather than by pos (rows past pos are never used). */
   const float qt = t < hs ? a.q[h * hs + t] : 0.0f;
+  float kv0[kChunk][kE];
+  key_rows(wave * kPerWave, a.seq_len, kv0);
+  float v0[kRows][kVec];
+#pragma unroll
+  for (int u = 0; u < kRows; ++u) {
+    row(g + u * kGroups, a.seq_len, v0[u]);
+  }
   const int pos = *a.pos;
   const int n = pos + 1;
   if (t < hs) {
     qs[t] = qt;
   }
   __syncthreads();
-  const float *kb = a.kcache + hk * hs;
-  const float *vb = a.vcache + hk * hs;
   const float root = sqrtf((float)hs);
-  const int sub = lane % kL;  /* this lane's slice of the head */
-  const int slot = lane / kL; /* which of the wave's positions */
   float qv[kE];
 #pragma unroll
   for (int e = 0; e < kE; ++e) {
     qv[e] = qs[sub * kE + e];
   }
-  /* kChunk rows of keys per lane in flight at once (a wave covers
-   * kChunk * kPerWave positions per round trip to memory). */
-  constexpr int kChunk = 8;
-  constexpr int kStride = 4 * kPerWave; /* positions between a wave's rows */
   float mx = -INFINITY;
-  for (int j0 = wave * kPerWave; j0 < n; j0 += kStride * kChunk) {
-    float kv[kChunk][kE];
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      const int j = j0 + c * kStride + slot;
-      if (j < n) {
-        const float *kr = kb + (int64_t)j * a.kv_dim + sub * kE;
-        if constexpr (kE == 4) {
-          const float4 v4 = *reinterpret_cast<const float4 *>(kr);
-          kv[c][0] = v4.x, kv[c][1] = v4.y, kv[c][2] = v4.z, kv[c][3] = v4.w;
-        } else {
-#pragma unroll
-          for (int e = 0; e < kE; ++e) {
-            kv[c][e] = kr[e];
-          }
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < kE; ++e) {
-          kv[c][e] = 0.0f;
-        }
-      }
-    }
+  auto score_chunk = [&](int j0, const float (&kv)[kChunk][kE]) {
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
       const int j = j0 + c * kStride + slot;
@@ -451,6 +491,12 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
         mx = fmaxf(mx, sc);
       }
     }
+  };
+  score_chunk(wave * kPerWave, kv0);
+  for (int j0 = wave * kPerWave + kStride * kChunk; j0 < n; j0 += kStride * kChunk) {
+    float kv[kChunk][kE];
+    key_rows(j0, n, kv);
+    score_chunk(j0, kv);
   }
   mx = block_max(mx, scratch); /* also orders the score writes */
   float sum = 0.0f;
@@ -460,39 +506,33 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
     sum += p;
   }
   sum = block_sum(sum, scratch); /* also orders the probability writes */
-  /* Values: a lane takes kVec consecutive elements of a position's row
-   * (float4 where the head allows), so a wave reads whole rows; the lane
-   * groups take positions round-robin, each adding its positions in
-   * increasing order with eight rows in flight, and meet in LDS. */
-  constexpr int kHs = kE * kL;
-  constexpr int kVec = (kHs % 4 == 0 && kHs >= 16) ? 4 : 1;
-  constexpr int kRowLanes = kHs / kVec;
-  constexpr int kGroups = kThreads / kRowLanes;
-  const int g = t / kRowLanes;
-  const int i = (t - g * kRowLanes) * kVec;
   float acc[kVec];
 #pragma unroll
   for (int e = 0; e < kVec; ++e) {
     acc[e] = 0.0f;
   }
-  auto row = [&](int jj, float (&v)[kVec]) {
-    const float *src = vb + (int64_t)jj * a.kv_dim + i;
-    if constexpr (kVec == 4) {
-      const float4 v4 = *reinterpret_cast<const float4 *>(src);
-      v[0] = v4.x, v[1] = v4.y, v[2] = v4.z, v[3] = v4.w;
-    } else {
-      v[0] = src[0];
-    }
-  };
-  int j = g;
-  for (; j + 7 * kGroups < n; j += 8 * kGroups) {
-    float v[8][kVec];
+  /* Each group adds its positions in increasing order: the preloaded rows
+   * first, then eight rows in flight at a time, then the tail. */
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      row(j + u * kGroups, v[u]);
+  for (int u = 0; u < kRows; ++u) {
+    const int jj = g + u * kGroups;
+    if (jj < n) {
+      const float p = score[jj];
+#pragma unroll
+      for (int e = 0; e < kVec; ++e) {
+        acc[e] = acc[e] + p * v0[u][e];
+      }
+    }
+  }
+  int j = g + kRows * kGroups;
+  for (; j + (kRows - 1) * kGroups < n; j += kRows * kGroups) {
+    float v[kRows][kVec];
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+      row(j + u * kGroups, n, v[u]);
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kRows; ++u) {
       const float p = score[j + u * kGroups];
 #pragma unroll
       for (int e = 0; e < kVec; ++e) {
@@ -502,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   }
   for (; j < n; j += kGroups) {
     float v[kVec];
-    row(j, v);
+    row(j, n, v);
     const float p = score[j];
 #pragma unroll
     for (int e = 0; e < kVec; ++e) {

@@ -57,6 +57,7 @@ struct StepAttnArgs {
   float *att;
   const int *pos;
   int kv_dim, hs, kv_mul;
+  int seq_len; /* rows of the cache (bounds loads issued before pos is known) */
 };
 
 
