@@ -189,76 +189,90 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   const int r0 = pair0 * 2; /* the first (for kPairs == 1, the only) pair */
   const bool live = r0 < a.rows;
 
-  /* The weights do not depend on x: request them first, so their latency
-   * runs under the normalisation below. */
+  /* Every load is a buffer load whose offset points past its range where
+   * the element does not exist (zeros come back), so no branch surrounds a
+   * load and the compiler can wait for exactly the loads it needs. Order
+   * of issue = order of arrival: first this thread's inputs (x and the norm
+   * weights, or the residual kernels' input vector), so the normalisation
+   * runs while the weights stream; then the weights; then the epilogue's
+   * operands (row scales; for the residual kernels the residual itself). */
+  constexpr uint32_t kOut = 0x80000000u; /* past every range */
+  constexpr int kPer = kCols / kThreads;
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.w, (short)0, a.rows * cols, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.scale, (short)0, a.rows * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(kMode == kResid ? a.in : a.x), (short)0, cols * 4, 0x00020000);
+  float xv[kPer], nv[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int i = t + k * kThreads;
+    xv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        xr, (int)(i < cols ? (uint32_t)(i * 4) : kOut), 0, 0));
+  }
+  if constexpr (kMode != kResid) {
+    const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.norm, (short)0, cols * 4, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      nv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          nr, (int)(i < cols ? (uint32_t)(i * 4) : kOut), 0, 0));
+    }
+  }
+
   u32x4 wp[kPairs][kSegs], wq[kPairs][kSegs];
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
     const int r = r0 + 2 * p;
     const bool ok_r = r < a.rows;
-    const int8_t *w0 = a.w + (int64_t)(ok_r ? r : 0) * cols;
 #pragma unroll
     for (int s = 0; s < kSegs; ++s) {
       const int c = s * 1024 + lane * 16;
       const bool ok = ok_r && c < cols;
-      wp[p][s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + c) : u32x4{0, 0, 0, 0};
-      wq[p][s] = ok ? *reinterpret_cast<const u32x4 *>(w0 + cols + c)
-                    : u32x4{0, 0, 0, 0};
+      const uint32_t off = ok ? (uint32_t)(r * cols + c) : kOut;
+      wp[p][s] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, 0);
+      wq[p][s] = __builtin_amdgcn_raw_buffer_load_b128(
+          wr, (int)(ok ? off + (uint32_t)cols : kOut), 0, 0);
     }
   }
 
-  /* The epilogue's operands (row scales; for the residual kernels the
-   * residual itself) do not depend on the GEMV either: requested now, so
-   * the epilogue does not wait a round trip for them. */
   float sc0[kPairs], sc1[kPairs];
 #pragma unroll
   for (int p = 0; p < kPairs; ++p) {
     const int r = r0 + 2 * p;
-    sc0[p] = r < a.rows ? a.scale[r] : 0.0f;
-    sc1[p] = r < a.rows ? a.scale[r + 1] : 0.0f;
+    const bool ok_r = r < a.rows;
+    sc0[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        sr, (int)(ok_r ? (uint32_t)(r * 4) : kOut), 0, 0));
+    sc1[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        sr, (int)(ok_r ? (uint32_t)(r * 4 + 4) : kOut), 0, 0));
   }
   float res0 = 0.0f, res1 = 0.0f;
   if constexpr (kMode == kResid) {
-    if (live) {
-      res0 = a.out[r0];
-      res1 = a.out[r0 + 1];
-    }
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.out, (short)0, a.rows * 4, 0x00020000);
+    res0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        rr, (int)(live ? (uint32_t)(r0 * 4) : kOut), 0, 0));
+    res1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        rr, (int)(live ? (uint32_t)(r0 * 4 + 4) : kOut), 0, 0));
   }
 
   float fcr = 0.0f, fci = 0.0f;
   int pos = 0;
   if constexpr (kMode == kResid) {
-    /* All of this thread's inputs in flight at once: a load-then-store
-     * loop would wait for each load in turn (and for the weights too, which
-     * were requested first). */
-    constexpr int kPer = kCols / kThreads;
-    float iv[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
-      iv[k] = i < cols ? a.in[i] : 0.0f;
-    }
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int i = t + k * kThreads;
       if (i < cols) {
-        xin[i] = iv[k];
+        xin[i] = xv[k];
       }
     }
   } else {
-    /* RMSNorm as reference examples/llama.vx:145-158; x and the norm
-     * weights are read once, into registers, alongside the weights. */
-    constexpr int kPer = kCols / kThreads;
-    float xv[kPer], nv[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
-      xv[k] = i < cols ? a.x[i] : 0.0f;
-      nv[k] = i < cols ? a.norm[i] : 0.0f;
-    }
-    /* The rotary factors of this wave's (even, odd) pair depend only on the
-     * position: requested behind the weights and x, so that chain of two
-     * loads runs under them instead of after the GEMV. */
+    /* RMSNorm as reference examples/llama.vx:145-158. The rotary factors
+     * of this wave's (even, odd) pair depend only on the position:
+     * requested behind the weights, so that chain of two loads runs under
+     * them instead of after the GEMV. */
     if constexpr (kMode == kQkv) {
       pos = *a.pos;
       if (live && r0 < a.dim + a.kv_dim) {
@@ -656,8 +670,9 @@ void launch_gemv(const StepGemvArgs &a, hipStream_t s) {
 } // namespace
 
 bool step_gemv_ok(int rows, int cols) {
+  /* The weights are one buffer range: rows * cols bytes in 31 bits. */
   return rows > 0 && rows % 2 == 0 && cols > 0 && cols % 16 == 0 &&
-         cols <= kMaxCols;
+         cols <= kMaxCols && (int64_t)rows * cols <= INT32_MAX;
 }
 
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kQkv>(a, s); }
