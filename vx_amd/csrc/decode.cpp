@@ -147,7 +147,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     at.q = m.q;
     at.kcache = g.kcache;
     at.vcache = g.vcache;
-    at.att = m.att;
+    at.part = m.att;
     at.pos = m.pos;
     at.kv_dim = m.kv_dim;
     at.hs = m.hs;
@@ -162,7 +162,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     wo.cols = c.dim;
     wo.in = m.att;
     wo.out = m.x;
-    vxk::step_gemv_resid(wo, m.stream);
+    vxk::step_gemv_attn_resid(wo, m.stream);
 
     vxk::StepGemvArgs ffn = g;
     ffn.w = m.w13 + (int64_t)l * 2 * c.hidden_dim * c.dim;
@@ -292,7 +292,7 @@ void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
   m->x = alloc<float>(*m, D);
   m->q = alloc<float>(*m, D);
   m->logits = alloc<float>(*m, (size_t)c.vocab_size);
-  m->att = alloc<float>(*m, D);
+  m->att = alloc<float>(*m, (size_t)vxk::attn_part_floats(c.dim, c.n_heads));
   m->hb = alloc<float>(*m, H);
   m->pos = alloc<int>(*m, 1);
   m->best = alloc<vxk::StepBest>(*m, (size_t)vxk::step_logits_groups(c.vocab_size));

@@ -7,9 +7,12 @@
  *
  *   step_gemv<kQkv>    RMSNorm(x), [Wq; Wk; Wv] int8 GEMV, RoPE on
  *                      q and k, k and v into the KV cache at `pos`
- *   step_attention     one workgroup per head: softmax(q k^T / sqrt(hs)) v
- *                      over positions 0..pos
- *   step_gemv<kResid>  x += Wo att
+ *   step_attention     kAttnSplit workgroups per head, each over every
+ *                      kAttnSplit-th position of 0..pos: its running max,
+ *                      sum of exponentials and unnormalised weighted sum of
+ *                      values (flash-decoding partials)
+ *   step_gemv<kAttnResid>  merges the partials into softmax(q k^T /
+ *                      sqrt(hs)) v on the way in, x += Wo att
  *   step_gemv<kSwiglu> RMSNorm(x), [W1; W3] GEMV with rows interleaved,
  *                      silu(h1) * h3
  *   step_gemv<kResid>  x += W2 h
@@ -166,7 +169,7 @@ __device__ void logits_best(const StepGemvArgs &a, Best b) {
   }
 }
 
-enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3 };
+enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4 };
 
 /* Row pairs per wave: the classifier's waves take several, so its
  * thousands of rows need fewer workgroups (one round over the CUs). */
@@ -188,6 +191,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   const int pair0 = (blockIdx.x * (kThreads / 64) + wave) * kPairs;
   const int r0 = pair0 * 2; /* the first (for kPairs == 1, the only) pair */
   const bool live = r0 < a.rows;
+  constexpr bool kRes = kMode == kResid || kMode == kAttnResid;
 
   /* Every load is a buffer load whose offset points past its range where
    * the element does not exist (zeros come back), so no branch surrounds a
@@ -202,16 +206,42 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       (void *)a.w, (short)0, a.rows * cols, 0x00020000);
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
       (void *)a.scale, (short)0, a.rows * 4, 0x00020000);
+  const int heads = kMode == kAttnResid ? cols / a.hs : 0;
+  const int in_bytes =
+      kMode == kAttnResid ? (kAttnSplit * cols + heads * kAttnSplit * 2) * 4 : cols * 4;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(kMode == kResid ? a.in : a.x), (short)0, cols * 4, 0x00020000);
+      (void *)(kRes ? a.in : a.x), (short)0, in_bytes, 0x00020000);
   float xv[kPer], nv[kPer];
+  /* Attention partials of this thread's columns: each split's sum, and the
+   * (max, sum) pairs of the column's head, all splits in two loads. */
+  float ov[kMode == kAttnResid ? kAttnSplit : 1][kPer];
+  u32x4 ml[kMode == kAttnResid ? kPer : 1][2];
+  if constexpr (kMode == kAttnResid) {
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int i = t + k * kThreads;
-    xv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        xr, (int)(i < cols ? (uint32_t)(i * 4) : kOut), 0, 0));
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      const bool ok = i < cols;
+#pragma unroll
+      for (int p = 0; p < kAttnSplit; ++p) {
+        ov[p][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            xr, (int)(ok ? (uint32_t)((p * cols + i) * 4) : kOut), 0, 0));
+      }
+      const uint32_t mo = (uint32_t)((kAttnSplit * cols + (i / a.hs) * kAttnSplit * 2) * 4);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        ml[k][q] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (int)(ok ? mo + 16 * q : kOut), 0, 0);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      xv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          xr, (int)(i < cols ? (uint32_t)(i * 4) : kOut), 0, 0));
+    }
   }
-  if constexpr (kMode != kResid) {
+  if constexpr (!kRes) {
     const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)a.norm, (short)0, cols * 4, 0x00020000);
 #pragma unroll
@@ -249,13 +279,18 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
         sr, (int)(ok_r ? (uint32_t)(r * 4 + 4) : kOut), 0, 0));
   }
   float res0 = 0.0f, res1 = 0.0f;
-  if constexpr (kMode == kResid) {
+  if constexpr (kRes) {
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)a.out, (short)0, a.rows * 4, 0x00020000);
     res0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         rr, (int)(live ? (uint32_t)(r0 * 4) : kOut), 0, 0));
     res1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         rr, (int)(live ? (uint32_t)(r0 * 4 + 4) : kOut), 0, 0));
+  }
+  if constexpr (kMode == kAttnResid) {
+    /* Keep the merge's arithmetic behind every load: scheduled earlier, it
+     * would wait for the partials before the weights are requested. */
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   float fcr = 0.0f, fci = 0.0f;
@@ -267,6 +302,35 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       if (i < cols) {
         xin[i] = xv[k];
       }
+    }
+  } else if constexpr (kMode == kAttnResid) {
+    /* softmax(scores) v = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M),
+     * M the largest split max (an empty split has m = -inf, l = o = 0). */
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = t + k * kThreads;
+      float mv[kAttnSplit], lv[kAttnSplit];
+#pragma unroll
+      for (int p = 0; p < kAttnSplit; ++p) {
+        mv[p] = __uint_as_float(ml[k][p >> 1][2 * (p & 1)]);
+        lv[p] = __uint_as_float(ml[k][p >> 1][2 * (p & 1) + 1]);
+      }
+      float mx = mv[0];
+#pragma unroll
+      for (int p = 1; p < kAttnSplit; ++p) {
+        mx = fmaxf(mx, mv[p]);
+      }
+      float num = 0.0f, den = 0.0f;
+#pragma unroll
+      for (int p = 0; p < kAttnSplit; ++p) {
+        const float w = expf(mv[p] - mx);
+        num = num + ov[p][k] * w;
+        den = den + lv[p] * w;
+      }
+      /* Stored whatever i (xin holds kCols >= cols floats; columns from
+       * cols on are never read): a branch here would let the compiler sink
+       * this column's loads behind the weights. */
+      xin[i] = num / den;
     }
   } else {
     /* RMSNorm as reference examples/llama.vx:145-158. The rotary factors
@@ -363,7 +427,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       a.vcache[(int64_t)pos * kv_dim + i] = y0;
       a.vcache[(int64_t)pos * kv_dim + i + 1] = y1;
     }
-  } else if constexpr (kMode == kResid) {
+  } else if constexpr (kRes) {
     a.out[r0] = res0 + y0;
     a.out[r0 + 1] = res1 + y1;
   } else if constexpr (kMode == kSwiglu) {
@@ -377,8 +441,12 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   }
 }
 
-/* One workgroup per query head over positions 0..pos (reference
- * :275-325); scores in dynamic LDS.
+/* Workgroup (h, sp) of query head h over positions sp, sp + kAttnSplit,
+ * ... up to pos (reference :275-325, split flash-decoding style so that
+ * kAttnSplit CUs share a head's key and value rows); scores in dynamic LDS,
+ * indexed by m for position sp + kAttnSplit m. It leaves its max M, its
+ * sum of e^(score - M) and its unnormalised weighted sum of values; the Wo
+ * GEMV merges the splits.
  *
  * Scores: kL lanes share a position, each taking kE consecutive elements of
  * the head (hs = kE * kL), so a wave reads 64 / kL whole key rows with one
@@ -400,6 +468,7 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   const int lane = t & 63;
   const int wave = t >> 6;
   const int h = blockIdx.x;
+  const int sp = blockIdx.y;
   const int hs = kE * kL;
   const int hk = h / a.kv_mul;
   const int sub = lane % kL;  /* this lane's slice of the head */
@@ -417,12 +486,13 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       (void *)a.vcache, (short)0, cache_bytes, 0x00020000);
   constexpr uint32_t kOut = 0x80000000u; /* past every range */
-  auto key_rows = [&](int j0, int bound, float (&kv)[kChunk][kE]) {
+  auto key_rows = [&](int m0, int bound, float (&kv)[kChunk][kE]) {
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
-      const int j = j0 + c * kStride + slot;
+      const int m = m0 + c * kStride + slot;
+      const int j = sp + kAttnSplit * m;
       const uint32_t off =
-          j < bound ? (uint32_t)((j * a.kv_dim + hk * hs + sub * kE) * 4) : kOut;
+          m < bound ? (uint32_t)((j * a.kv_dim + hk * hs + sub * kE) * 4) : kOut;
       if constexpr (kE == 4) {
         const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)off, 0, 0);
 #pragma unroll
@@ -448,10 +518,12 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   constexpr int kRows = 8; /* value rows per lane in flight */
   const int g = t / kRowLanes;
   const int i = (t - g * kRowLanes) * kVec;
-  /* Row jj of this lane's values, zeros from jj >= bound. */
-  auto row = [&](int jj, int bound, float (&v)[kVec]) {
+  /* Value row of local index mm (position sp + kAttnSplit mm), zeros from
+   * mm >= bound. */
+  auto row = [&](int mm, int bound, float (&v)[kVec]) {
+    const int jj = sp + kAttnSplit * mm;
     const uint32_t off =
-        jj < bound ? (uint32_t)((jj * a.kv_dim + hk * hs + i) * 4) : kOut;
+        mm < bound ? (uint32_t)((jj * a.kv_dim + hk * hs + i) * 4) : kOut;
     if constexpr (kVec == 4) {
       const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)off, 0, 0);
 #pragma unroll
@@ -467,15 +539,17 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
    * on the position: they are requested together with it, bounded by the
    * cache's length rather than by pos (rows past pos are never used). */
   const float qt = t < hs ? a.q[h * hs + t] : 0.0f;
+  const int ms = (a.seq_len - sp + kAttnSplit - 1) / kAttnSplit; /* split's rows < seq_len */
   float kv0[kChunk][kE];
-  key_rows(wave * kPerWave, a.seq_len, kv0);
+  key_rows(wave * kPerWave, ms, kv0);
   float v0[kRows][kVec];
 #pragma unroll
   for (int u = 0; u < kRows; ++u) {
-    row(g + u * kGroups, a.seq_len, v0[u]);
+    row(g + u * kGroups, ms, v0[u]);
   }
   const int pos = *a.pos;
-  const int n = pos + 1;
+  /* This split's positions: sp + kAttnSplit m for m < n (none if sp > pos). */
+  const int n = pos >= sp ? (pos - sp) / kAttnSplit + 1 : 0;
   if (t < hs) {
     qs[t] = qt;
   }
@@ -490,7 +564,7 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   auto score_chunk = [&](int j0, const float (&kv)[kChunk][kE]) {
 #pragma unroll
     for (int c = 0; c < kChunk; ++c) {
-      const int j = j0 + c * kStride + slot;
+      const int j = j0 + c * kStride + slot; /* local index */
       float dot = 0.0f;
 #pragma unroll
       for (int e = 0; e < kE; ++e) {
@@ -568,13 +642,17 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
     part[g * kHs + i + e] = acc[e];
   }
   __syncthreads();
+  const int dim = gridDim.x * hs;
   if (t < hs) {
     float o = 0.0f;
     for (int gg = 0; gg < kGroups; ++gg) {
       o += part[gg * kHs + t];
     }
-    const float inv = 1.0f / sum;
-    a.att[h * hs + t] = o * inv;
+    a.part[sp * dim + h * hs + t] = o;
+  }
+  if (t == 0) {
+    a.part[kAttnSplit * dim + (h * kAttnSplit + sp) * 2] = mx;
+    a.part[kAttnSplit * dim + (h * kAttnSplit + sp) * 2 + 1] = sum;
   }
 }
 
@@ -677,6 +755,9 @@ bool step_gemv_ok(int rows, int cols) {
 
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kQkv>(a, s); }
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kResid>(a, s); }
+void step_gemv_attn_resid(const StepGemvArgs &a, hipStream_t s) {
+  launch_gemv<kAttnResid>(a, s);
+}
 void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kSwiglu>(a, s); }
 void step_gemv_logits(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kLogits>(a, s); }
 
@@ -690,16 +771,17 @@ void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
 
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
                            hipStream_t s) {
-  const size_t lds = (size_t)seq_len * sizeof(float);
+  const size_t lds = (size_t)((seq_len + kAttnSplit - 1) / kAttnSplit) * sizeof(float);
+  const dim3 grid(heads, kAttnSplit);
   switch (a.hs) {
-  case 2: hipLaunchKernelGGL((step_attention<2, 1>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  case 4: hipLaunchKernelGGL((step_attention<4, 1>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  case 8: hipLaunchKernelGGL((step_attention<4, 2>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  case 16: hipLaunchKernelGGL((step_attention<4, 4>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  case 32: hipLaunchKernelGGL((step_attention<4, 8>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  case 64: hipLaunchKernelGGL((step_attention<4, 16>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  case 128: hipLaunchKernelGGL((step_attention<4, 32>), dim3(heads), dim3(kThreads), lds, s, a); break;
-  default: hipLaunchKernelGGL((step_attention<4, 64>), dim3(heads), dim3(kThreads), lds, s, a); break;
+  case 2: hipLaunchKernelGGL((step_attention<2, 1>), grid, dim3(kThreads), lds, s, a); break;
+  case 4: hipLaunchKernelGGL((step_attention<4, 1>), grid, dim3(kThreads), lds, s, a); break;
+  case 8: hipLaunchKernelGGL((step_attention<4, 2>), grid, dim3(kThreads), lds, s, a); break;
+  case 16: hipLaunchKernelGGL((step_attention<4, 4>), grid, dim3(kThreads), lds, s, a); break;
+  case 32: hipLaunchKernelGGL((step_attention<4, 8>), grid, dim3(kThreads), lds, s, a); break;
+  case 64: hipLaunchKernelGGL((step_attention<4, 16>), grid, dim3(kThreads), lds, s, a); break;
+  case 128: hipLaunchKernelGGL((step_attention<4, 32>), grid, dim3(kThreads), lds, s, a); break;
+  default: hipLaunchKernelGGL((step_attention<4, 64>), grid, dim3(kThreads), lds, s, a); break;
   }
 }
 

@@ -40,7 +40,8 @@ struct StepGemvArgs {
   int rows, cols;
   const float *x;      /* residual stream, normalised on the way in */
   const float *norm;   /* RMSNorm weight */
-  const float *in;     /* input vector (residual mode) */
+  const float *in;     /* input vector (residual modes; the Wo GEMV reads
+                          the attention partials and merges them) */
   float *out;          /* q, x (accumulated) or logits */
   float *hout;         /* SwiGLU output */
   float *kcache, *vcache; /* this layer's [seq, kv_dim] */
@@ -51,10 +52,21 @@ struct StepGemvArgs {
   StepBest *part;
 };
 
+/* Workgroups per head in step_attention: split s takes positions s,
+ * s + kAttnSplit, s + 2 kAttnSplit, ... and the Wo GEMV merges the splits. */
+constexpr int kAttnSplit = 4;
+
+/* Floats of the attention partials for a model of `dim` = heads * hs:
+ * [kAttnSplit][dim] unnormalised weighted value sums, then
+ * [heads][kAttnSplit] (running max, sum of exponentials) pairs. */
+inline int64_t attn_part_floats(int dim, int heads) {
+  return (int64_t)kAttnSplit * dim + (int64_t)heads * kAttnSplit * 2;
+}
+
 struct StepAttnArgs {
   const float *q;
   const float *kcache, *vcache;
-  float *att;
+  float *part; /* attn_part_floats(heads * hs, heads) */
   const int *pos;
   int kv_dim, hs, kv_mul;
   int seq_len; /* rows of the cache (bounds loads issued before pos is known) */
@@ -65,6 +77,8 @@ struct StepAttnArgs {
 bool step_gemv_ok(int rows, int cols);
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s);
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s);
+/* x += Wo merge(attention partials); cols = heads * hs, hs dividing cols. */
+void step_gemv_attn_resid(const StepGemvArgs &a, hipStream_t s);
 void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s);
 /* The classifier; leaves step_logits_groups(rows) StepBest entries in
  * `part` for step_choose_launch. */
