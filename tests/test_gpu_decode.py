@@ -37,11 +37,15 @@ def assert_same_tokens(got, want, margin):
                                              n_kv_heads=6, vocab_size=512, seq_len=64),
                                  # head size 128
                                  LlamaConfig(dim=1024, hidden_dim=2816, n_layers=1, n_heads=8,
-                                             n_kv_heads=8, vocab_size=384, seq_len=48)])
+                                             n_kv_heads=8, vocab_size=384, seq_len=48),
+                                 # a cache length that the attention split does not divide,
+                                 # filled to its last row
+                                 LlamaConfig(dim=96, hidden_dim=160, n_layers=2, n_heads=3,
+                                             n_kv_heads=1, vocab_size=200, seq_len=37)])
 def test_logits_per_position_match_oracle(hiplib, cfg):
     announce(f"decode logits {cfg}")
     weights = make_model(cfg, seed=3)
-    tokens = list(make_prompt(cfg, n=20, seed=5))
+    tokens = list(make_prompt(cfg, n=cfg.seq_len if cfg.seq_len < 40 else 20, seed=5))
     model = LlamaI8(hiplib, cfg, weights)
     got = model.logits(tokens)
     model.close()

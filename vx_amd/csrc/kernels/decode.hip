@@ -173,7 +173,12 @@ enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4 };
 
 /* Row pairs per wave: the classifier's waves take several, so its
  * thousands of rows need fewer workgroups (one round over the CUs). */
-template <int kMode> constexpr int pairs_per_wave() { return kMode == 3 ? 4 : 1; }
+#ifndef VX_DEC_LOGIT_PAIRS
+#define VX_DEC_LOGIT_PAIRS 4
+#endif
+template <int kMode> constexpr int pairs_per_wave() {
+  return kMode == 3 ? VX_DEC_LOGIT_PAIRS : 1;
+}
 
 /* kSegs: 1024-column segments the kernel is built for (cols <= 1024 kSegs),
  * so registers and LDS are sized to the matrix rather than to kMaxCols. */
@@ -213,9 +218,9 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       (void *)(kRes ? a.in : a.x), (short)0, in_bytes, 0x00020000);
   float xv[kPer], nv[kPer];
   /* Attention partials of this thread's columns: each split's sum, and the
-   * (max, sum) pairs of the column's head, all splits in two loads. */
+   * (max, sum) pairs of the column's head, two splits per load. */
   float ov[kMode == kAttnResid ? kAttnSplit : 1][kPer];
-  u32x4 ml[kMode == kAttnResid ? kPer : 1][2];
+  u32x4 ml[kMode == kAttnResid ? kPer : 1][kAttnSplit / 2];
   if constexpr (kMode == kAttnResid) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       }
       const uint32_t mo = (uint32_t)((kAttnSplit * cols + (i / a.hs) * kAttnSplit * 2) * 4);
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int q = 0; q < kAttnSplit / 2; ++q) {
         ml[k][q] = __builtin_amdgcn_raw_buffer_load_b128(
             xr, (int)(ok ? mo + 16 * q : kOut), 0, 0);
       }

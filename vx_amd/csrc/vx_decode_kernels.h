@@ -53,8 +53,13 @@ struct StepGemvArgs {
 };
 
 /* Workgroups per head in step_attention: split s takes positions s,
- * s + kAttnSplit, s + 2 kAttnSplit, ... and the Wo GEMV merges the splits. */
-constexpr int kAttnSplit = 4;
+ * s + kAttnSplit, s + 2 kAttnSplit, ... and the Wo GEMV merges the splits.
+ * (2, 4 and 8 decode config 4 within run-to-run noise of one another.) */
+#ifndef VX_ATTN_SPLIT
+#define VX_ATTN_SPLIT 4
+#endif
+constexpr int kAttnSplit = VX_ATTN_SPLIT;
+static_assert(kAttnSplit % 2 == 0, "the merge reads (max, sum) pairs two splits at a time");
 
 /* Floats of the attention partials for a model of `dim` = heads * hs:
  * [kAttnSplit][dim] unnormalised weighted value sums, then
