@@ -289,6 +289,11 @@ void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
   m->rope = upload(*m, w->rope, (size_t)c.seq_len * hs);
   m->kcache = alloc<float>(*m, L * (size_t)c.seq_len * KV);
   m->vcache = alloc<float>(*m, L * (size_t)c.seq_len * KV);
+  /* Rows past the position are read (and discarded) by the attention
+   * kernels' early loads: start them at zero rather than at whatever the
+   * allocation held. */
+  VX_HIP_CHECK(hipMemset(m->kcache, 0, L * (size_t)c.seq_len * KV * sizeof(float)));
+  VX_HIP_CHECK(hipMemset(m->vcache, 0, L * (size_t)c.seq_len * KV * sizeof(float)));
   m->x = alloc<float>(*m, D);
   m->q = alloc<float>(*m, D);
   m->logits = alloc<float>(*m, (size_t)c.vocab_size);

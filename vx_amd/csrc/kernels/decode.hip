@@ -661,6 +661,190 @@ __global__ __launch_bounds__(kThreads) void step_attention(StepAttnArgs a) {
   }
 }
 
+/* Sum over the lanes that share lane % kL (partners at xor kL, 2 kL, ...,
+ * 32), each an exact xor pairing for kL >= 8. */
+template <int kL> __device__ __forceinline__ float slot_sum(float v) {
+  static_assert(kL >= 8 && kL <= 64, "xor partners from 8 up");
+  if constexpr (kL <= 8) v += partner<8>(v);
+  if constexpr (kL <= 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                    __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (kL <= 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                    __float_as_uint(v), false,
+                                                    false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return v;
+}
+
+/* The same partials as step_attention for heads of 32 to 256 (kL = hs / 4
+ * lanes per position, 4 elements each), with each wave's softmax kept in
+ * registers: the kL lanes that score a position also hold that position's
+ * value row (the same float4 slice of it), so the probability never leaves
+ * them. Wave w takes the split's local rows w * 64/kL + slot + c * 256/kL
+ * (c < 8), keys and values requested together; rounds of 8 rows per lane
+ * repeat with the usual online rescale while positions remain. The four
+ * waves' (max, sum, weighted values) then meet once in LDS. */
+template <int kL>
+__global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) {
+#pragma clang fp contract(off)
+  constexpr int kE = 4;
+  constexpr int hs = kE * kL;
+  constexpr int kPerWave = 64 / kL;       /* positions a wave scores at once */
+  constexpr int kChunk = 8;               /* rows per lane in flight */
+  constexpr int kStride = 4 * kPerWave;   /* local rows between a wave's rows */
+  constexpr int kRound = kStride * kChunk; /* local rows per round */
+  __shared__ float wo[4][hs];
+  __shared__ float wm[4], wl[4];
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int h = blockIdx.x;
+  const int sp = blockIdx.y;
+  const int hk = h / a.kv_mul;
+  const int sub = lane % kL;
+  const int slot = lane / kL;
+  constexpr uint32_t kOut = 0x80000000u; /* past every range */
+  const int cache_bytes = a.seq_len * a.kv_dim * 4;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.kcache, (short)0, cache_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.vcache, (short)0, cache_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)a.q, (short)0, (int)gridDim.x * hs * 4, 0x00020000);
+  const uint32_t col = (uint32_t)((hk * hs + sub * kE) * 4);
+  /* Key and value slices of this lane's rows of round r0; zeros from local
+   * row `bound` on. */
+  auto load_rows = [&](int r0, int bound, u32x4 (&kw)[kChunk], u32x4 (&vw)[kChunk]) {
+    const int m0 = r0 + wave * kPerWave + slot;
+    const uint32_t row_bytes = (uint32_t)a.kv_dim * 4;
+    const uint32_t base = (uint32_t)(sp + kAttnSplit * m0) * row_bytes + col;
+    const uint32_t step = (uint32_t)(kStride * kAttnSplit) * row_bytes;
+    uint32_t off[kChunk];
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      off[c] = m0 + c * kStride < bound ? base + (uint32_t)c * step : kOut;
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      kw[c] = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)off[c], 0, 0);
+    }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      vw[c] = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)off[c], 0, 0);
+    }
+  };
+
+  /* q and the first round's rows do not depend on the position: requested
+   * with it, bounded by the cache's length (rows past pos are never used). */
+  const u32x4 qw = __builtin_amdgcn_raw_buffer_load_b128(
+      qrs, (int)((h * hs + sub * kE) * 4), 0, 0);
+  const int ms = (a.seq_len - sp + kAttnSplit - 1) / kAttnSplit;
+  u32x4 kw[kChunk], vw[kChunk];
+  load_rows(0, ms, kw, vw);
+  const int pos = *a.pos;
+  const int n = pos >= sp ? (pos - sp) / kAttnSplit + 1 : 0;
+  const float root = sqrtf((float)hs);
+  float q[kE];
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    q[e] = __uint_as_float(qw[e]);
+  }
+  float m_run = -INFINITY, l_run = 0.0f, acc[kE];
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    acc[e] = 0.0f;
+  }
+  for (int r0 = 0;; r0 += kRound) {
+    float sc[kChunk];
+    float mr = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int m = r0 + wave * kPerWave + c * kStride + slot;
+      float dot = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kE; ++e) {
+        dot = dot + q[e] * __uint_as_float(kw[c][e]);
+      }
+      dot = group_sum<kL>(dot);
+      sc[c] = dot / root;
+      mr = m < n ? fmaxf(mr, sc[c]) : mr;
+    }
+    mr = wave_max(mr);
+    const float mnew = fmaxf(m_run, mr);
+    if (mnew != -INFINITY) { /* wave-uniform: some row of this wave is live */
+      const float alpha = expf(m_run - mnew); /* 0 while m_run is -inf */
+      float ps = 0.0f;
+#pragma unroll
+      for (int e = 0; e < kE; ++e) {
+        acc[e] = acc[e] * alpha;
+      }
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c) {
+        const int m = r0 + wave * kPerWave + c * kStride + slot;
+        const bool live = m < n;
+        const float p = live ? expf(sc[c] - mnew) : 0.0f;
+        ps = ps + p;
+        /* Rows from n on were loaded (bounded by the cache's length) but
+         * never written: their bits may be Inf or NaN, and 0 * Inf is NaN,
+         * so they are selected away rather than multiplied by zero. */
+#pragma unroll
+        for (int e = 0; e < kE; ++e) {
+          const float pv = p * __uint_as_float(vw[c][e]);
+          acc[e] = acc[e] + (live ? pv : 0.0f);
+        }
+      }
+      l_run = l_run * alpha + ps;
+      m_run = mnew;
+    }
+    if (r0 + kRound >= n) {
+      break;
+    }
+    load_rows(r0 + kRound, n, kw, vw);
+  }
+  /* Every lane of a slot holds that slot's sums: add the slots. */
+  l_run = slot_sum<kL>(l_run);
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    acc[e] = slot_sum<kL>(acc[e]);
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int e = 0; e < kE; ++e) {
+      wo[wave][sub * kE + e] = acc[e];
+    }
+  }
+  if (lane == 0) {
+    wm[wave] = m_run;
+    wl[wave] = l_run;
+  }
+  __syncthreads();
+  const int dim = gridDim.x * hs;
+  if (t < hs) {
+    float mx = wm[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      mx = fmaxf(mx, wm[w]);
+    }
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - mx);
+      o = o + wo[w][t] * f;
+      l = l + wl[w] * f;
+    }
+    a.part[sp * dim + h * hs + t] = o;
+    if (t == 0) {
+      a.part[kAttnSplit * dim + (h * kAttnSplit + sp) * 2] = mx;
+      a.part[kAttnSplit * dim + (h * kAttnSplit + sp) * 2 + 1] = l;
+    }
+  }
+}
+
 constexpr int kChooseThreads = 1024;
 
 /* Merge the classifier workgroups' partials: argmax with the lowest index
@@ -707,7 +891,9 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
         a.out_margin[at] = r.v1 - r.v2;
       }
     }
-    chosen = tok;
+    /* Every logit NaN leaves no winner (index 0x7fffffff): read row 0
+     * rather than past the table; the NaN margin reports it. */
+    chosen = tok >= 0 && tok < a.vocab ? tok : 0;
   }
   __syncthreads();
   const int tok = chosen;
@@ -783,10 +969,10 @@ void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
   case 4: hipLaunchKernelGGL((step_attention<4, 1>), grid, dim3(kThreads), lds, s, a); break;
   case 8: hipLaunchKernelGGL((step_attention<4, 2>), grid, dim3(kThreads), lds, s, a); break;
   case 16: hipLaunchKernelGGL((step_attention<4, 4>), grid, dim3(kThreads), lds, s, a); break;
-  case 32: hipLaunchKernelGGL((step_attention<4, 8>), grid, dim3(kThreads), lds, s, a); break;
-  case 64: hipLaunchKernelGGL((step_attention<4, 16>), grid, dim3(kThreads), lds, s, a); break;
-  case 128: hipLaunchKernelGGL((step_attention<4, 32>), grid, dim3(kThreads), lds, s, a); break;
-  default: hipLaunchKernelGGL((step_attention<4, 64>), grid, dim3(kThreads), lds, s, a); break;
+  case 32: hipLaunchKernelGGL((step_attention_rows<8>), grid, dim3(kThreads), 0, s, a); break;
+  case 64: hipLaunchKernelGGL((step_attention_rows<16>), grid, dim3(kThreads), 0, s, a); break;
+  case 128: hipLaunchKernelGGL((step_attention_rows<32>), grid, dim3(kThreads), 0, s, a); break;
+  default: hipLaunchKernelGGL((step_attention_rows<64>), grid, dim3(kThreads), 0, s, a); break;
   }
 }
 
