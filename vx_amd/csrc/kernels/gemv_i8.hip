@@ -489,6 +489,15 @@ void launch_b4(const int8_t *w, const float *s, const uint16_t *x, float *y,
  * 4096-column passes. Measured best: 4 rows for batch 1 (against 1, 2, 8 and
  * 16) and 16 for batch 2 (against 4 and 8): x costs the workgroup 2 * kB
  * bytes per column, the weights kR. */
+/* Rows per workgroup at batch 1, for rows of at most kGroupCols columns and
+ * for longer ones. */
+#ifndef VX_GEMV_B1_R
+#define VX_GEMV_B1_R 4
+#endif
+#ifndef VX_GEMV_B1_RLONG
+#define VX_GEMV_B1_RLONG 4
+#endif
+
 template <int kB, int kR>
 void launch_rows(const int8_t *w, const float *s, const uint16_t *x, float *y,
                  int rows, int cols, int nb, hipStream_t stream) {
@@ -527,7 +536,11 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
    * operand, read once per 16 (or, for batches of 8 and more over 8192 rows
    * and more, 64) rows. */
   if (nb == 1) {
-    launch_rows<1, 4>(w, scale, x, y, r, c, nb, stream);
+    if (c > kGroupCols) {
+      launch_rows<1, VX_GEMV_B1_RLONG>(w, scale, x, y, r, c, nb, stream);
+    } else {
+      launch_rows<1, VX_GEMV_B1_R>(w, scale, x, y, r, c, nb, stream);
+    }
   } else if (nb == 2 && c <= kGroupCols) {
     launch_rows<2, 16>(w, scale, x, y, r, c, nb, stream);
   } else if (nb <= 4 && c <= kGroupCols) {
