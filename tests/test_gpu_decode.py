@@ -138,3 +138,27 @@ def test_model_read_from_checkpoint_file_generates_like_oracle(hiplib, tmp_path)
     got2, _ = model.generate(prompt, 30)
     model.close()
     assert list(map(int, got2)) == list(map(int, got))
+
+
+@pytest.mark.parametrize("cfg,n", [
+    # head size 256: a split's rounds hold 32 positions, so 150 positions take two
+    (LlamaConfig(dim=512, hidden_dim=256, n_layers=1, n_heads=2, n_kv_heads=1,
+                 vocab_size=256, seq_len=160), 150),
+    # head size 64 (config 4's): rounds of 128 per split, 560 positions take two
+    (LlamaConfig(dim=128, hidden_dim=256, n_layers=1, n_heads=2, n_kv_heads=2,
+                 vocab_size=256, seq_len=576), 560)])
+def test_long_sequence_logits_match_oracle(hiplib, cfg, n):
+    """Caches long enough that each attention workgroup rescales its running
+    softmax between rounds of key and value rows."""
+    announce(f"decode long logits {cfg} n={n}")
+    weights = make_model(cfg, seed=4)
+    tokens = list(make_prompt(cfg, n=n, seed=6))
+    model = LlamaI8(hiplib, cfg, weights)
+    got = model.logits(tokens)
+    model.close()
+    kv = np.zeros(2 * cfg.n_layers * cfg.seq_len * cfg.kv_dim, np.float32)
+    for pos, tok in enumerate(tokens):
+        want = oracle.llama_forward(cfg.as_dict(), weights, kv, int(tok), pos)
+        scale = float(np.abs(want).max())
+        err = float(np.abs(got[pos] - want).max())
+        assert err <= 1e-3 * scale + 1e-5, f"position {pos}: max abs error {err} (scale {scale})"
