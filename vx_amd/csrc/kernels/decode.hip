@@ -173,6 +173,10 @@ enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4 };
 
 /* Row pairs per wave: the classifier's waves take several, so its
  * thousands of rows need fewer workgroups (one round over the CUs). */
+/* Cache policy of the weight loads (0: default; 2: non-temporal). */
+#ifndef VX_DEC_W_CPOL
+#define VX_DEC_W_CPOL 0
+#endif
 #ifndef VX_DEC_LOGIT_PAIRS
 #define VX_DEC_LOGIT_PAIRS 4
 #endif
@@ -267,9 +271,9 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       const int c = s * 1024 + lane * 16;
       const bool ok = ok_r && c < cols;
       const uint32_t off = ok ? (uint32_t)(r * cols + c) : kOut;
-      wp[p][s] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, 0);
+      wp[p][s] = __builtin_amdgcn_raw_buffer_load_b128(wr, (int)off, 0, VX_DEC_W_CPOL);
       wq[p][s] = __builtin_amdgcn_raw_buffer_load_b128(
-          wr, (int)(ok ? off + (uint32_t)cols : kOut), 0, 0);
+          wr, (int)(ok ? off + (uint32_t)cols : kOut), 0, VX_DEC_W_CPOL);
     }
   }
 
