@@ -30,7 +30,7 @@ struct LlamaI8 {
   float *tok_s = nullptr, *sqkv = nullptr, *so = nullptr, *s13 = nullptr,
         *s2 = nullptr;
   float *rms_att = nullptr, *rms_ffn = nullptr, *rms_final = nullptr,
-        *rope = nullptr;
+        *rope = nullptr, *rope_now = nullptr;
   float *kcache = nullptr, *vcache = nullptr;
   float *x = nullptr, *q = nullptr, *logits = nullptr;
   float *att = nullptr, *hb = nullptr;
@@ -115,6 +115,10 @@ vxk::StepArgmaxArgs argmax_args(LlamaI8 &m, int n_prompt) {
   a.tok_s = m.tok_s;
   a.x = m.x;
   a.dim = m.cfg.dim;
+  a.rope = m.rope;
+  a.rope_now = m.rope_now;
+  a.hs = m.hs;
+  a.seq_len = m.cfg.seq_len;
   return a;
 }
 
@@ -129,7 +133,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     g.dim = c.dim;
     g.kv_dim = m.kv_dim;
     g.hs = m.hs;
-    g.rope = m.rope;
+    g.rope = m.rope_now;
     g.kcache = m.kcache + l * layer_kv;
     g.vcache = m.vcache + l * layer_kv;
 
@@ -287,6 +291,7 @@ void *vx_llama_i8_create(const vx_llama_i8_config *cfg,
   m->rms_ffn = upload(*m, w->rms_ffn, L * D);
   m->rms_final = upload(*m, w->rms_final, D);
   m->rope = upload(*m, w->rope, (size_t)c.seq_len * hs);
+  m->rope_now = alloc<float>(*m, (size_t)hs);
   m->kcache = alloc<float>(*m, L * (size_t)c.seq_len * KV);
   m->vcache = alloc<float>(*m, L * (size_t)c.seq_len * KV);
   /* Rows past the position are read (and discarded) by the attention

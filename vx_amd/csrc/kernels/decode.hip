@@ -302,8 +302,22 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
+  /* The rotary factors of this wave's (even, odd) pair at this step's
+   * position: step_choose (step_start at position 0) leaves that row of the
+   * table in a.rope, so they are requested behind the weights without
+   * waiting for the position. */
   float fcr = 0.0f, fci = 0.0f;
   int pos = 0;
+  if constexpr (kMode == kQkv) {
+    const __amdgpu_buffer_rsrc_t ropr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.rope, (short)0, a.hs * 4, 0x00020000);
+    const int i = r0 < a.dim ? r0 : r0 - a.dim;
+    const bool rot = live && r0 < a.dim + a.kv_dim;
+    const uint32_t roff = rot ? (uint32_t)((i % a.hs) * 4) : kOut;
+    fcr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ropr, (int)roff, 0, 0));
+    fci = __uint_as_float(
+        __builtin_amdgcn_raw_buffer_load_b32(ropr, (int)(rot ? roff + 4 : kOut), 0, 0));
+  }
   if constexpr (kMode == kResid) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -342,19 +356,9 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       xin[i] = num / den;
     }
   } else {
-    /* RMSNorm as reference examples/llama.vx:145-158. The rotary factors
-     * of this wave's (even, odd) pair depend only on the position:
-     * requested behind the weights, so that chain of two loads runs under
-     * them instead of after the GEMV. */
+    /* RMSNorm as reference examples/llama.vx:145-158. */
     if constexpr (kMode == kQkv) {
-      pos = *a.pos;
-      if (live && r0 < a.dim + a.kv_dim) {
-        const int i = r0 < a.dim ? r0 : r0 - a.dim;
-        const int hd = i % a.hs;
-        const float *cs = a.rope + ((int64_t)pos * (a.hs / 2) + hd / 2) * 2;
-        fcr = cs[0];
-        fci = cs[1];
-      }
+      pos = *a.pos; /* where k and v go in the cache */
     }
     float ss = 0.0f;
 #pragma unroll
@@ -863,6 +867,13 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int pos = *a.pos;
+  /* The next step's row of the rotary table (pairs for every head offset);
+   * none past the cache, where no step follows. */
+  if (pos + 1 < a.seq_len) {
+    for (int i = t; i < a.hs; i += kChooseThreads) {
+      a.rope_now[i] = a.rope[(int64_t)(pos + 1) * a.hs + i];
+    }
+  }
   Best b{-INFINITY, 0x7fffffff, -INFINITY};
   for (int i = t; i < nparts; i += kChooseThreads) {
     b = merge(b, part[i]);
@@ -910,8 +921,12 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
   }
 }
 
-/* Position 0: the first prompt token's embedding. */
+/* Position 0: the first prompt token's embedding and row 0 of the rotary
+ * table. */
 __global__ void step_start(StepArgmaxArgs a) {
+  for (int i = threadIdx.x; i < a.hs; i += blockDim.x) {
+    a.rope_now[i] = a.rope[i];
+  }
   const int tok = a.prompt[0];
   const float s = a.tok_s[tok];
   for (int i = threadIdx.x; i < a.dim; i += blockDim.x) {

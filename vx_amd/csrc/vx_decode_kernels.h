@@ -25,6 +25,11 @@ struct StepArgmaxArgs {
   const float *tok_s;
   float *x;
   int dim;
+  /* The rotary table [seq_len, hs/2, 2] and the row of it for the next
+   * step, which the QKV GEMVs read. */
+  const float *rope;
+  float *rope_now;
+  int hs, seq_len;
 };
 
 /* Best and runner-up logit of a workgroup's rows (classifier epilogue). */
@@ -45,7 +50,7 @@ struct StepGemvArgs {
   float *out;          /* q, x (accumulated) or logits */
   float *hout;         /* SwiGLU output */
   float *kcache, *vcache; /* this layer's [seq, kv_dim] */
-  const float *rope;   /* [seq, hs/2, 2] */
+  const float *rope;   /* this step's row of the rotary table: [hs/2, 2] */
   const int *pos;
   int dim, kv_dim, hs;
   /* Classifier only: one StepBest per workgroup. */
