@@ -193,22 +193,29 @@ static inline uint64_t vx_memref_view_bytes(const int64_t *sizes,
   if (why == VX_VIEW_OK) {
     return bytes;
   }
-  if (why == VX_VIEW_UNKNOWN_ELEMENT) {
+  switch (why) {
+  case VX_VIEW_UNKNOWN_ELEMENT:
+    /* Code 0 is what the compiler writes for index and pointer elements. */
     fprintf(stderr,
-            "[Vx] FATAL: the runtime cannot copy a tensor with the element "
-            "type code %d, because it does not know the size of the element. "
-            "The compiler writes code 0 for index and pointer elements\n",
+            "[Vx] FATAL: no byte size is known for element type %d (index "
+            "and pointer elements carry code 0), so a view of it cannot be "
+            "copied\n",
             elem);
-  } else if (why == VX_VIEW_NEGATIVE) {
-    fprintf(stderr,
-            "[Vx] FATAL: dimension %d of a tensor view has the negative "
-            "%s %lld\n",
-            d, sizes[d] < 0 ? "size" : "stride",
-            (long long)(sizes[d] < 0 ? sizes[d] : strides[d]));
-  } else if (why == VX_VIEW_TOO_MANY_ELEMENTS) {
-    fprintf(stderr, "[Vx] FATAL: a tensor view spans 2^64 elements or more\n");
-  } else {
-    fprintf(stderr, "[Vx] FATAL: a tensor view spans 2^64 bytes or more\n");
+    break;
+  case VX_VIEW_NEGATIVE:
+    fprintf(stderr, "[Vx] FATAL: broken view descriptor: %s %lld in "
+                    "dimension %d is below zero\n",
+            sizes[d] < 0 ? "size" : "stride",
+            (long long)(sizes[d] < 0 ? sizes[d] : strides[d]), d);
+    break;
+  case VX_VIEW_TOO_MANY_ELEMENTS:
+    fprintf(stderr, "[Vx] FATAL: broken view descriptor: its element count "
+                    "does not fit in 64 bits\n");
+    break;
+  default:
+    fprintf(stderr, "[Vx] FATAL: broken view descriptor: its byte span does "
+                    "not fit in 64 bits\n");
+    break;
   }
   abort();
 }

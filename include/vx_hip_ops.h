@@ -35,7 +35,8 @@ enum {
   VX_OP_EINVAL = -1,   /* an extent, stride or argument is out of range */
   VX_OP_ENODEV = -2,   /* no GPU: this library has no host copy of the op */
   VX_OP_ENOTDEV = -3,  /* a pointer is not device memory */
-  VX_OP_EUNSUPP = -4   /* a shape the kernels do not take */
+  VX_OP_EUNSUPP = -4,  /* a shape the kernels do not take */
+  VX_OP_ENOMEM = -5    /* host or device memory ran out */
 };
 
 /* Flash-attention forward (the op packages/vx_nn/lib.vx declares).

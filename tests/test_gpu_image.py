@@ -175,3 +175,43 @@ def test_host_operands_take_the_host_path(hiplib, host_axpy, rng):
     (st1, fb1) = counters(hiplib)
     assert np.array_equal(y, want)
     assert st1["launches"] == st0["launches"] and fb1 == fb0 + 1
+
+
+TIMED = r"""
+import sys
+sys.path.insert(0, {root!r})
+import numpy as np
+from vx_amd import abi
+from vx_amd.build import TEST_IMAGES
+from vx_amd.runtime import DispatchLibrary, DeviceArray
+lib = DispatchLibrary()
+n = 4096
+x = np.arange(n, dtype=np.float32)
+dx, dy = DeviceArray.of(lib, x, abi.DTYPE_F32), DeviceArray.of(lib, x, abi.DTYPE_F32)
+args = abi.CallArgs()
+args.memref(dx.descriptor(), abi.DTYPE_F32).memref(dy.descriptor(), abi.DTYPE_F32)
+args.scalar(2.0, abi.KIND_F32)
+img = (TEST_IMAGES / "vx_image_kernels.hsaco").read_bytes()
+lib.dispatch(abi.image_payload("vx_img_axpy", img, topo="500", launch=str(n)), args)
+assert np.array_equal(dy.numpy(), 3 * x)
+print("ok", flush=True)
+"""
+
+
+def test_time_kernel_brackets_image_launches():
+    """VX_TIME_KERNEL prints the device time of an image launch, not only of
+    a routed GEMM (reference runtime/cuda_dispatch.cpp:1613-1665); run in a
+    child process so the variable is read fresh."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    announce("VX_TIME_KERNEL on an image launch")
+    root = Path(__file__).resolve().parent.parent
+    res = subprocess.run([sys.executable, "-c", TIMED.format(root=str(root))],
+                         capture_output=True, text=True, timeout=120,
+                         env={**os.environ, "VX_TIME_KERNEL": "1"})
+    assert res.returncode == 0 and "ok" in res.stdout, res.stderr[-2000:]
+    assert "vx_img_axpy device time" in res.stderr, res.stderr[-2000:]
+    assert "vx_img_axpy occupancy" in res.stderr, res.stderr[-2000:]

@@ -104,6 +104,16 @@ void _vx_ciface_vx_test_kernel_0(D2 *a, float s, D2 *out) {
       out->aligned[out->offset + i * out->strides[0] + j * out->strides[1]] =
           a->aligned[a->offset + i * a->strides[0] + j * a->strides[1]] * s + 1.0f;
 }
+/* a `launch=` region split over host workers: each worker takes every
+ * count-th row from its id, and records its id and the worker count */
+int64_t vx_host_worker_id(void);
+int64_t vx_host_worker_count(void);
+void _vx_ciface_vx_test_kernel_2(D2 *out) {
+  for (int64_t i = vx_host_worker_id(); i < out->sizes[0]; i += vx_host_worker_count()) {
+    out->aligned[out->offset + i * out->strides[0]] = (float)vx_host_worker_id();
+    out->aligned[out->offset + i * out->strides[0] + 1] = (float)vx_host_worker_count();
+  }
+}
 /* the outlined loop nest of a classified matmul (used when no GPU runs it) */
 void _vx_ciface_vx_test_kernel_1(D2 *a, int64_t i0, D2 *b, int64_t i1, float fill, D2 *c) {
   for (int64_t i = 0; i < a->sizes[0]; ++i)
@@ -140,6 +150,29 @@ def test_unrouted_dispatch_runs_the_outlined_host_kernel(cpulib, outlined):
     args.memref(abi.Descriptor(out.ctypes.data, out.shape), abi.DTYPE_F32)
     cpulib.dispatch(abi.payload("vx_test_kernel_0", abi="1", topo="500"), args)
     assert np.array_equal(out, a * 2.5 + 1)
+
+
+@pytest.mark.parametrize("threads,payload_entries,want", [
+    ("3", {"launch": "12"}, 3),           # VX_HOST_THREADS wins
+    ("100", {"launch": "12"}, 12),        # never more workers than iterations
+    ("0", {"launch": "12"}, 1),           # 0 (or nonsense) is serial
+    ("4", {"launch": "12,64"}, 1),        # the two-level form is not split
+    ("4", {}, 1),                         # an unproven region is not split
+    ("4", {"host_blocks": "1", "grid": "6", "block": "32"}, 4),
+])
+def test_split_regions_run_on_host_workers(cpulib, outlined, monkeypatch, threads,
+                                           payload_entries, want):
+    """`launch=`/`host_blocks=` regions run on VX_HOST_THREADS workers, each
+    reading its slice from vx_host_worker_id/count (reference
+    runtime/vx_host_call.h:132-238)."""
+    monkeypatch.setenv("VX_HOST_THREADS", threads)
+    out = np.full((12, 2), -1, np.float32)
+    args = abi.CallArgs()
+    args.memref(abi.Descriptor(out.ctypes.data, out.shape), abi.DTYPE_F32)
+    cpulib.dispatch(abi.payload("vx_test_kernel_2", abi="1", **payload_entries), args)
+    assert np.all(out[:, 1] == want), out
+    assert np.array_equal(out[:, 0], np.arange(12) % want), out
+    assert cpulib.lib.vx_host_worker_id() == 0 and cpulib.lib.vx_host_worker_count() == 1
 
 
 def test_matmul_without_a_gpu_runs_the_outlined_loop(cpulib, outlined):

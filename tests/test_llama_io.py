@@ -125,3 +125,18 @@ def test_refusals(lib, tmp_path):
     (tmp_path / "flip.q8").write_bytes(bytes(q8))
     with pytest.raises(OSError):
         read_model(lib, tmp_path / "flip.q8")
+
+
+def test_huge_vxq8_header_is_refused_before_allocating(lib, tmp_path):
+    """A VXQ8 header that claims the largest config the reader accepts (dim
+    2^16, hidden 2^18, 4096 layers, vocab 2^22) on a file of a few bytes is
+    refused from the size check, without allocating the terabytes the
+    header describes."""
+    save_model(lib, tmp_path / "m.q8", CFG, llama.make_model(CFG))
+    q8 = bytearray((tmp_path / "m.q8").read_bytes())
+    q8[8:36] = np.array([1 << 16, 1 << 18, 4096, 1 << 10, 1 << 10, 1 << 22, 1 << 20],
+                        dtype=np.int32).tobytes()
+    (tmp_path / "huge.q8").write_bytes(bytes(q8))
+    with pytest.raises(OSError) as e:
+        read_model(lib, tmp_path / "huge.q8")
+    assert e.value.args[0] == -1  # VX_OP_EINVAL: size disagrees with header

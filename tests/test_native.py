@@ -1,7 +1,8 @@
 """Builds and runs the GPU-free C++ unit tests of the vendor-free headers
 (tests/native/*.cpp), as the reference's runtime tests are built and run
 (reference tests/integration_test/runtime_test_build.rs: -Wall -Werror, and
-ASan/UBSan on request)."""
+ASan/UBSan on request). The host-fallback test calls through libffi, so every
+test is linked with the image's libffi, as the dispatch library is."""
 
 import os
 import subprocess
@@ -11,13 +12,16 @@ import pytest
 
 HERE = Path(__file__).resolve().parent
 NATIVE = HERE / "native"
+FFI_INC = Path("/opt/conda/include")
+FFI_LIB = Path("/usr/lib/x86_64-linux-gnu/libffi.so.8")
 
 
 @pytest.mark.parametrize("src", sorted(p.name for p in NATIVE.glob("*_test.cpp")))
 @pytest.mark.parametrize("sanitize", [False, True])
 def test_native(src, sanitize, tmp_path):
     exe = tmp_path / src.replace(".cpp", "")
-    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Werror", str(NATIVE / src), "-o", str(exe)]
+    cmd = ["g++", "-std=c++17", "-O1", "-Wall", "-Werror", f"-I{FFI_INC}", str(NATIVE / src),
+           "-o", str(exe), str(FFI_LIB), "-ldl", "-lpthread"]
     if sanitize:
         cmd[1:1] = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer"]
     subprocess.run(cmd, check=True)

@@ -26,9 +26,18 @@
  * default the null stream), as the reference does (:205-207). A launch
  * returns at once; waits happen at read-backs, awaits and VX_CTRL_WAIT*.
  *
+ * Waits (vx_stream_policy.h): a wait covers the caller stream, or every
+ * device this library used when none is set; while the caller stream is
+ * capturing a hipGraph, anything that must block the host is refused with a
+ * message. A wait that finds a fault names the last kernel launched there.
+ * With a caller stream, HBM from vx_plugin_alloc_and_transfer is taken and
+ * given back in that stream's order (hipMallocAsync / hipFreeAsync).
+ *
  * Environment: VX_DISPATCH_VERBOSE (routing narrative on stderr),
- * VX_TIME_KERNEL (device time of each routed GEMM on stderr), VX_HIP_SYNC=1
- * (wait after every launch, so a fault names its launch), VX_HIP_POOL_MAX_MB.
+ * VX_TIME_KERNEL (device time of each routed GEMM and image launch on
+ * stderr), VX_HIP_SYNC=1 (wait after every launch, so a fault names its
+ * launch), VX_HIP_POOL_MAX_MB, VX_HOST_THREADS (host workers of a split
+ * region on the host).
  */
 #include "../../include/vx_hardware_runtime.h"
 #include "../../include/vx_hip_ops.h"
@@ -39,6 +48,7 @@
 #include "vx_image_launch.h"
 #include "vx_kernels.h"
 #include "vx_ops_internal.h"
+#include "vx_stream_policy.h"
 
 #include <dlfcn.h>
 
@@ -160,22 +170,181 @@ Pool &pool() {
   return *p;
 }
 
+/* The last kernel each device started that no wait has covered yet, so that
+ * a wait that finds a fault can name a suspect (reference
+ * runtime/cuda_dispatch.cpp:190-300). VX_HIP_SYNC=1 waits after every launch
+ * instead, which names the faulting kernel itself. */
+std::mutex unwaited_mutex;
+std::map<int, std::string> &unwaited() {
+  static auto *m = new std::map<int, std::string>();
+  return *m;
+}
+/* The last kernel this thread started on its caller stream. */
+thread_local std::string last_on_stream;
+
+/* HBM this library took with hipMallocAsync on a caller's stream: freed in
+ * that stream's order (hipFreeAsync), also once the caller has moved on to
+ * another stream. */
+std::mutex stream_allocs_mutex;
+std::map<void *, hipStream_t> &stream_allocs() {
+  static auto *m = new std::map<void *, hipStream_t>();
+  return *m;
+}
+
+/* Whether the caller's stream is being captured into a hipGraph now. */
+bool capturing() {
+  if (!caller_stream) {
+    return false;
+  }
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(caller_stream, &status);
+  if (e != hipSuccess) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: cannot tell whether the stream given to "
+            "vx_hip_set_stream is capturing a graph: %s\n",
+            hipGetErrorString(e));
+    abort();
+  }
+  return status != hipStreamCaptureStatusNone;
+}
+
+/* `what` cannot be recorded into the graph the caller's stream is capturing;
+ * `fix` says what the program can do instead. */
+[[noreturn]] void refuse_in_capture(
+    const char *what,
+    const char *fix = "Pass only tensors already in GPU memory while the "
+                      "capture runs, and read results after it ends.") {
+  fprintf(stderr,
+          "[Vx HIP] FATAL: %s while the stream given to vx_hip_set_stream is "
+          "capturing a hipGraph, and a graph cannot record that. %s\n",
+          what, fix);
+  abort();
+}
+
+/* Waits for every device this library launched on (the current one always),
+ * naming the last kernel started there when one faulted. */
+void wait_for_devices() {
+  std::map<int, std::string> started;
+  {
+    std::lock_guard<std::mutex> hold(unwaited_mutex);
+    started.swap(unwaited());
+  }
+  int current = 0;
+  VX_HIP_CHECK(hipGetDevice(&current));
+  started.emplace(current, std::string());
+  for (const auto &entry : started) {
+    if (entry.first != current) {
+      VX_HIP_CHECK(hipSetDevice(entry.first));
+    }
+    const hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      fprintf(stderr,
+              "[Vx HIP] FATAL: GPU %d reported a fault: %s. Last kernel "
+              "launched there: %s (VX_HIP_SYNC=1 waits after each launch to "
+              "name the one that faulted)\n",
+              entry.first, hipGetErrorString(e),
+              entry.second.empty() ? "none by this library"
+                                   : entry.second.c_str());
+      abort();
+    }
+  }
+  VX_HIP_CHECK(hipSetDevice(current));
+}
+
+/* Waits for the work before `why`: the caller's stream if one is set, else
+ * every device this library used. */
 void wait_for_kernels(const char *why) {
   if (verbose()) {
     fprintf(stderr, "[Vx HIP] wait: %s\n", why);
   }
-  hipError_t e = caller_stream ? hipStreamSynchronize(caller_stream)
-                               : hipDeviceSynchronize();
+  switch (vx::wait_action(caller_stream != nullptr, capturing())) {
+  case vx::WaitAction::kDevice:
+    wait_for_devices();
+    return;
+  case vx::WaitAction::kRefuse: {
+    char what[256];
+    snprintf(what, sizeof what, "a wait for the GPU (%s) came", why);
+    refuse_in_capture(what);
+  }
+  case vx::WaitAction::kStream:
+    break;
+  }
+  const hipError_t e = hipStreamSynchronize(caller_stream);
   if (e != hipSuccess) {
-    fprintf(stderr, "[Vx HIP] FATAL: a GPU launch failed (%s) before %s\n",
-            hipGetErrorString(e), why);
+    fprintf(stderr,
+            "[Vx HIP] FATAL: the stream given to vx_hip_set_stream reported a "
+            "fault (%s) before %s. Last kernel launched on it: %s "
+            "(VX_HIP_SYNC=1 waits after each launch to name the one that "
+            "faulted)\n",
+            hipGetErrorString(e), why,
+            last_on_stream.empty() ? "none by this library"
+                                   : last_on_stream.c_str());
     abort();
   }
 }
 
-void started_kernel(const char *what) {
+/* After a launch of `name` on the current device. */
+void started_kernel(const char *name) {
+  int device = 0;
+  VX_HIP_CHECK(hipGetDevice(&device));
   if (sync_each_launch()) {
-    wait_for_kernels(what);
+    if (capturing()) {
+      refuse_in_capture("VX_HIP_SYNC=1 asked for a wait after a launch",
+                        "Unset VX_HIP_SYNC while capturing.");
+    }
+    const hipError_t e = caller_stream ? hipStreamSynchronize(caller_stream)
+                                       : hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      fprintf(stderr, "[Vx HIP] FATAL: %s faulted on GPU %d: %s\n", name,
+              device, hipGetErrorString(e));
+      abort();
+    }
+    return;
+  }
+  if (caller_stream) {
+    last_on_stream = name;
+  }
+  std::lock_guard<std::mutex> hold(unwaited_mutex);
+  unwaited()[device] = name;
+}
+
+/* HBM of `bytes`, in stream order on the caller's stream when one is set. */
+hipError_t device_alloc(void **ptr, size_t bytes) {
+  if (!caller_stream) {
+    return hipMalloc(ptr, bytes);
+  }
+  const hipError_t e = hipMallocAsync(ptr, bytes, caller_stream);
+  if (e == hipSuccess) {
+    std::lock_guard<std::mutex> hold(stream_allocs_mutex);
+    stream_allocs()[*ptr] = caller_stream;
+  }
+  return e;
+}
+
+/* Frees HBM from vx_plugin_alloc_and_transfer / transfer_peer. */
+void device_free(void *ptr) {
+  hipStream_t from = nullptr;
+  bool ordered = false;
+  {
+    std::lock_guard<std::mutex> hold(stream_allocs_mutex);
+    auto found = stream_allocs().find(ptr);
+    if (found != stream_allocs().end()) {
+      from = found->second;
+      ordered = true;
+      stream_allocs().erase(found);
+    }
+  }
+  switch (vx::free_action(caller_stream != nullptr, capturing(), ordered)) {
+  case vx::FreeAction::kOnStream:
+    VX_HIP_CHECK(hipFreeAsync(ptr, from));
+    return;
+  case vx::FreeAction::kRefuse:
+    refuse_in_capture("GPU memory that a launch may still read was freed");
+  case vx::FreeAction::kAfterDeviceWait:
+  case vx::FreeAction::kAfterStreamWait:
+    wait_for_kernels("a device buffer was freed");
+    VX_HIP_CHECK(hipFree(ptr));
+    return;
   }
 }
 
@@ -210,6 +379,9 @@ void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
     out.ptr = const_cast<void *>(data);
     out.row_stride = row_stride;
     return;
+  }
+  if (capturing()) {
+    refuse_in_capture("a GEMM operand in host memory was copied to the GPU");
   }
   const size_t width = (size_t)cols * esz;
   out.bytes = (size_t)rows * width;
@@ -279,6 +451,10 @@ bool run_gemm(const vx_gemm_plan &plan) {
   }
 
   const bool time_kernel = getenv("VX_TIME_KERNEL") != nullptr;
+  if (time_kernel && capturing()) {
+    refuse_in_capture("VX_TIME_KERNEL waits for each kernel",
+                      "Unset VX_TIME_KERNEL while capturing.");
+  }
   hipEvent_t t0 = nullptr, t1 = nullptr;
   if (time_kernel) {
     VX_HIP_CHECK(hipEventCreate(&t0));
@@ -336,12 +512,16 @@ bool run_gemm(const vx_gemm_plan &plan) {
 vx::HostCopies host_copies() {
   vx::HostCopies io;
   io.is_device = [](const void *p) { return is_device_ptr(p); };
-  io.to_host = [](void *dst, const void *src, size_t n) {
-    wait_for_kernels("a host kernel read GPU memory");
-    VX_HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyDeviceToHost));
+  io.sync = [] { wait_for_kernels("a host kernel read GPU memory"); };
+  io.to_host = [](void *dst, size_t dpitch, const void *src, size_t spitch,
+                  size_t width, size_t height) {
+    VX_HIP_CHECK(hipMemcpy2D(dst, dpitch, src, spitch, width, height,
+                             hipMemcpyDeviceToHost));
   };
-  io.to_device = [](void *dst, const void *src, size_t n) {
-    VX_HIP_CHECK(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+  io.to_device = [](void *dst, size_t dpitch, const void *src, size_t spitch,
+                    size_t width, size_t height) {
+    VX_HIP_CHECK(hipMemcpy2D(dst, dpitch, src, spitch, width, height,
+                             hipMemcpyHostToDevice));
   };
   return io;
 }
@@ -529,6 +709,25 @@ bool run_device_image(const void *payload, size_t payload_size,
   const unsigned shared =
       shared_field ? (unsigned)strtoul(shared_field, nullptr, 10) : 0u;
   const char *coop = vx_payload_field(payload, payload_size, "coop=");
+  /* Device time of the launch on request, stamped by hipEvents on the launch
+   * stream (the same instrument as a routed GEMM's). */
+  const bool time_kernel = getenv("VX_TIME_KERNEL") != nullptr;
+  if (time_kernel && capturing()) {
+    refuse_in_capture("VX_TIME_KERNEL waits for each kernel",
+                      "Unset VX_TIME_KERNEL while capturing.");
+  }
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  if (time_kernel) {
+    int resident = 0;
+    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(
+            &resident, loaded.fn, (int)block, shared) == hipSuccess) {
+      fprintf(stderr, "[Vx HIP] %s occupancy: %d workgroup(s) of %u per CU\n",
+              name, resident, block);
+    }
+    VX_HIP_CHECK(hipEventCreate(&t0));
+    VX_HIP_CHECK(hipEventCreate(&t1));
+    VX_HIP_CHECK(hipEventRecord(t0, caller_stream));
+  }
   hipError_t e;
   if (coop && strcmp(coop, "0") != 0) {
     /* Grid-wide barriers: every block must be resident at once, which the
@@ -546,6 +745,16 @@ bool run_device_image(const void *payload, size_t payload_size,
     abort();
   }
   started_kernel(name);
+  if (time_kernel) {
+    VX_HIP_CHECK(hipEventRecord(t1, caller_stream));
+    VX_HIP_CHECK(hipEventSynchronize(t1));
+    float ms = 0.0f;
+    VX_HIP_CHECK(hipEventElapsedTime(&ms, t0, t1));
+    fprintf(stderr, "[Vx HIP] %s device time %.3f ms (%ux%ux%u x %u)\n", name,
+            ms, grid[0], grid[1], grid[2], block);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+  }
   ++stat_image_launches;
   if (takes_flag) {
     int failed = 0;
@@ -587,9 +796,29 @@ void run_on_host(const void *payload, size_t payload_size, void **device_args,
             kind ? kind : "<unclassified>");
   }
   ++stat_host_fallback;
-  if (!vx::call_on_host(kernel, device_args, arg_tags, num_args,
-                        host_copies())) {
+  const int workers = vx::host_worker_count_for(payload, payload_size,
+                                                device_args, arg_tags, num_args);
+  int64_t bad = -1;
+  const int rc = vx::call_on_host(
+      kernel, device_args, arg_tags, num_args, workers,
+      vx::host_flushes_subnormals(payload, payload_size), host_copies(), &bad);
+  if (rc == 0) {
     fprintf(stderr, "[Vx HIP] FATAL: could not build a call for %s\n", name);
+    abort();
+  }
+  if (rc == -1) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: argument %lld of %s is a GPU view with a negative "
+            "offset or one that runs past the end of the address space\n",
+            (long long)bad, name);
+    abort();
+  }
+  if (rc == -2) {
+    fprintf(stderr,
+            "[Vx HIP] FATAL: %s published through argument %lld a view into a "
+            "host copy of GPU memory that has no layout in the GPU tensor it "
+            "was copied from\n",
+            name, (long long)bad);
     abort();
   }
 }
@@ -708,8 +937,11 @@ void *vx_plugin_alloc_and_transfer(size_t bytes, void *host_ptr,
     }
   }
   void *p = nullptr;
-  VX_HIP_CHECK(hipMalloc(&p, bytes ? bytes : 1));
+  VX_HIP_CHECK(device_alloc(&p, bytes ? bytes : 1));
   if (host_ptr && bytes) {
+    if (capturing()) {
+      refuse_in_capture("a tensor in host memory was copied to the GPU");
+    }
     if (caller_stream) {
       VX_HIP_CHECK(hipMemcpyAsync(p, host_ptr, bytes, hipMemcpyHostToDevice,
                                   caller_stream));
@@ -846,7 +1078,7 @@ void *vx_plugin_transfer_peer(void *src_device_ptr, uint32_t src_topology_id,
   }
   select_device((int32_t)dst_topology_id, "peer");
   void *p = nullptr;
-  VX_HIP_CHECK(hipMalloc(&p, bytes ? bytes : 1));
+  VX_HIP_CHECK(device_alloc(&p, bytes ? bytes : 1));
   if (bytes) {
     if (src == dst) {
       VX_HIP_CHECK(hipMemcpyAsync(p, src_device_ptr, bytes,
@@ -869,9 +1101,7 @@ void vx_plugin_free(void *device_ptr, uint32_t topology_id) {
   }
   if (is_device_ptr(device_ptr)) {
     select_device((int32_t)topology_id, "free");
-    /* A launch still reading the buffer must end first. */
-    wait_for_kernels("a device buffer was freed");
-    VX_HIP_CHECK(hipFree(device_ptr));
+    device_free(device_ptr);
   } else {
     free(device_ptr);
   }
@@ -1079,7 +1309,7 @@ void vx_collective_all_gather_bf16(const uint16_t *input, uint16_t *output,
   one_rank_copy(input, output, count, 2, "vx_collective_all_gather_bf16");
 }
 
-int64_t vx_host_worker_id(void) { return 0; }
-int64_t vx_host_worker_count(void) { return 1; }
+int64_t vx_host_worker_id(void) { return vx::host_worker_index; }
+int64_t vx_host_worker_count(void) { return vx::host_worker_total; }
 
 } // extern "C"

@@ -266,19 +266,25 @@ int32_t read_q8(const std::vector<unsigned char> &b, vx_llama_i8_host &h) {
   if (!config_ok(c)) {
     return fail(VX_OP_EINVAL, "VXQ8 header is not a usable config");
   }
-  h.cfg = c;
-  size_all(h);
-  rope_table(c, h.rope);
-  size_t payload = 0;
-  for (const Field &f : fields(h)) {
-    payload += f.bytes;
-  }
-  const size_t body = 8 + 28 + payload;
-  if (b.size() != body + 8) {
+  /* The payload's size follows from the header alone; it is compared with
+   * the file before anything is allocated, so a corrupt header cannot ask
+   * for more memory than the file holds. Every count fits in int64 within
+   * config_ok's limits. */
+  const int64_t d = c.dim, hd = c.hidden_dim, L = c.n_layers;
+  const int64_t kv = d * c.n_kv_heads / c.n_heads;
+  const int64_t rows = (int64_t)c.vocab_size + L * (3 * d + 2 * kv + 2 * hd);
+  const int64_t int8s = (int64_t)c.vocab_size * d + L * (2 * d * d + 2 * kv * d + 3 * hd * d);
+  const int64_t norms = L * 2 * d + d;
+  const uint64_t payload = (uint64_t)int8s + 4 * (uint64_t)(rows + norms);
+  const uint64_t body = 8 + 28 + payload;
+  if ((uint64_t)b.size() != body + 8) {
     return fail(VX_OP_EINVAL, "VXQ8 file size " + std::to_string(b.size()) +
                                   " does not match its header (expected " +
                                   std::to_string(body + 8) + ")");
   }
+  h.cfg = c;
+  size_all(h);
+  rope_table(c, h.rope);
   uint64_t want;
   memcpy(&want, b.data() + body, 8);
   if (fnv1a(b.data(), body) != want) {
@@ -309,10 +315,18 @@ int32_t vx_llama_i8_read(const char *path, vx_llama_i8_config *cfg,
   if (bytes.size() < 28) {
     return fail(VX_OP_EINVAL, std::string(path) + " is too short for a model");
   }
-  vx_llama_i8_host *h = new vx_llama_i8_host();
-  const int32_t rc = memcmp(bytes.data(), kMagic, 4) == 0
-                         ? read_q8(bytes, *h)
-                         : read_checkpoint(bytes, *h);
+  vx_llama_i8_host *h = new (std::nothrow) vx_llama_i8_host();
+  if (!h) {
+    return fail(VX_OP_ENOMEM, "out of host memory for a model");
+  }
+  int32_t rc;
+  try {
+    rc = memcmp(bytes.data(), kMagic, 4) == 0 ? read_q8(bytes, *h)
+                                              : read_checkpoint(bytes, *h);
+  } catch (const std::bad_alloc &) {
+    /* No exception may cross the C boundary. */
+    rc = fail(VX_OP_ENOMEM, std::string("out of host memory reading ") + path);
+  }
   if (rc != VX_OP_OK) {
     delete h;
     return rc;
