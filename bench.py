@@ -39,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+PEAK_CLOCK_MHZ = 2400.0    # the clock the bf16 peak is quoted at
 
 
 def log(msg: str) -> None:
@@ -58,6 +59,28 @@ def traffic_from_profiles(name: str):
 
 
 SETTLE_MS = 200.0  # untimed GPU work before each kernel's warmup steps
+
+
+def spread(xs) -> dict:
+    """Median, fastest and slowest of a list of timings (every run kept in
+    the summary, as the reference's benchmarking policy asks)."""
+    xs = sorted(xs)
+    return dict(median=round(float(np.median(xs)), 3), min=round(xs[0], 3),
+                max=round(xs[-1], 3), n=len(xs))
+
+
+def timed_runs(call, timer, steps: int, runs: int = 3, stream=None) -> list:
+    """`runs` timed regions of `steps` calls each; the per-call milliseconds
+    of each region (hipEvents on the launch stream)."""
+    out = []
+    for _ in range(runs):
+        e0, e1 = timer.event(), timer.event()
+        timer.record(e0, stream)
+        for _ in range(steps):
+            call()
+        timer.record(e1, stream)
+        out.append(timer.elapsed_ms(e0, e1) / steps)
+    return out
 
 
 def settle(call, timer, min_ms: float = SETTLE_MS) -> float:
@@ -107,15 +130,27 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     for _ in range(warmup):
         dispatch(buf, len(pl), argv, tags, nargs)
     timer.sync()
-    e0, e1 = timer.event(), timer.event()
+    # Clock stamps of the timed launches (workgroup 0's shader-clock and
+    # 100 MHz real-time counters at its start and end), one slot per step.
+    stamps = lib.transfer(None, 32 * steps)
+    lib.clock_stamps(stamps, steps)
+    events = [timer.event() for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    timer.record(e0)
-    for _ in range(steps):
+    timer.record(events[0])
+    for i in range(steps):
         dispatch(buf, len(pl), argv, tags, nargs)
-    timer.record(e1)
-    ms_events = timer.elapsed_ms(e0, e1)
+        timer.record(events[i + 1])
+    ms_events = timer.elapsed_ms(events[0], events[-1])
     timer.sync()
     wall = time.perf_counter() - t0
+    lib.clock_stamps(None, 0)
+    step_ms = [timer.elapsed_ms(events[i], events[i + 1]) for i in range(steps)]
+    st = np.empty((steps, 4), np.uint64)
+    lib.fetch(stamps, st)
+    lib.free(stamps)
+    clk = (st[:, 2] - st[:, 0]).astype(np.float64)
+    rt = (st[:, 3] - st[:, 1]).astype(np.float64)
+    clock_mhz = float(clk.sum() / rt.sum() * 100.0) if rt.sum() > 0 else None
     after = lib.stats()
     assert after["gemm_mfma"] - before["gemm_mfma"] == steps + warmup + settled[0], \
         "GEMM did not take the MFMA path"
@@ -126,7 +161,8 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     flops = 2.0 * n * n * n
     ms_step = ms_events / steps
     return dict(n=n, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / steps,
-                tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16)
+                tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16,
+                steps_us=spread([x * 1e3 for x in step_ms]), clock_mhz=clock_mhz)
 
 
 def bench_gemm_f32(lib, timer, steps: int = 50, n: int = 512):
@@ -255,17 +291,19 @@ def bench_fa(lib, timer, steps: int, warmup: int):
     for _ in range(warmup):
         call()
     timer.sync()
-    e0, e1 = timer.event(), timer.event()
-    timer.record(e0)
-    for _ in range(steps):
-        call()
-    timer.record(e1)
-    ms = timer.elapsed_ms(e0, e1) / steps
+    runs = timed_runs(call, timer, steps)
+    ms = float(np.median(runs))
     for x in arrs + [do, dl]:
         x.free()
     flops = 2.0 * b * h * s * s * d  # causal: half of 4*B*H*S^2*D
-    return dict(config="causal [4,32,2048,128] bf16", ms=ms, tflops=flops / (ms * 1e-3) / 1e12,
-                frac_of_peak=flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return dict(config="causal [4,32,2048,128] bf16", ms=ms, tflops=tflops,
+                frac_of_peak=tflops / PEAK_BF16_TFLOPS,
+                runs_us=spread([x * 1e3 for x in runs]), steps_per_run=steps,
+                roofline={"bound": "mfma", "achieved": round(tflops, 2),
+                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                          "traffic": traffic_from_profiles("fa_causal_4x32x2048x128")})
 
 
 def bench_gemv(lib, timer, steps: int, warmup: int):
@@ -315,17 +353,19 @@ def bench_gemv(lib, timer, steps: int, warmup: int):
                 graph = timer.capture(stream, calls)
                 timer.graph_launch(graph, stream)  # warm
                 reps = 4
-                timer.record(e0, stream)
-                for _ in range(reps):
+                ev = [timer.event() for _ in range(reps + 1)]
+                timer.record(ev[0], stream)
+                for r in range(reps):
                     timer.graph_launch(graph, stream)
-                timer.record(e1, stream)
-                us = timer.elapsed_ms(e0, e1) / (reps * n_calls) * 1e3
+                    timer.record(ev[r + 1], stream)
+                us = timer.elapsed_ms(ev[0], ev[-1]) / (reps * n_calls) * 1e3
+                per_rep = [timer.elapsed_ms(ev[r], ev[r + 1]) / n_calls * 1e3 for r in range(reps)]
                 timer.graph_destroy(graph)
                 nbytes = rows * cols + 4 * rows + 2 * batch * cols + 4 * batch * rows
                 gbs = nbytes / (us * 1e-6) / 1e9
                 out.append(dict(shape=[rows, cols], batch=batch, us=us, gbs=gbs,
                                 frac_of_hbm=gbs / PEAK_HBM_GBS, us_eager=us_eager,
-                                rotated_copies=copies))
+                                runs_us=spread(per_rep), rotated_copies=copies))
                 x.free()
                 y.free()
             for a in ws + [sc]:
@@ -404,7 +444,8 @@ def main() -> int:
 
     log(f"gemm bf16->f32 4096^3: warmup {ns.warmup}, steps {ns.steps}")
     g = bench_gemm(lib, timer, ns.steps, ns.warmup)
-    log(f"gemm {g['tflops']:.1f} TFLOP/s ({g['ms_per_step'] * 1e3:.1f} us/step)")
+    log(f"gemm {g['tflops']:.1f} TFLOP/s ({g['ms_per_step'] * 1e3:.1f} us/step, clock "
+        f"{g['clock_mhz'] or 0:.0f} MHz)")
 
     extra = {}
     if "fa" in only:
@@ -429,7 +470,8 @@ def main() -> int:
         log("gemm bf16->f32 8192^3 (roofline point)")
         g8 = bench_gemm(lib, timer, 10, 2, n=8192)
         extra["gemm_bf16_8192"] = dict(config="bf16 x bf16 -> f32 GEMM, M=N=K=8192", ms=g8["ms_per_step"],
-                                       tflops=g8["tflops"], frac_of_peak=g8["tflops"] / PEAK_BF16_TFLOPS)
+                                       tflops=g8["tflops"], frac_of_peak=g8["tflops"] / PEAK_BF16_TFLOPS,
+                                       steps_us=g8["steps_us"], clock_mhz=g8["clock_mhz"])
         log(f"gemm 8192 {g8['tflops']:.1f} TFLOP/s")
         log("gemm f32 512^3 (config 1)")
         extra["gemm_f32_512"] = bench_gemm_f32(lib, timer)
@@ -467,9 +509,16 @@ def main() -> int:
         "config": {"workload": "bf16 x bf16 -> f32 GEMM, M=N=K=4096 (BASELINE config 2), "
                                "operands resident in HBM, one vx_plugin_dispatch_async per step",
                    "m": 4096, "n": 4096, "k": 4096},
+        "steps_us": g["steps_us"],
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_from_profiles("gemm_bf16_4096")},
+                     "traffic": traffic_from_profiles("gemm_bf16_4096"),
+                     # the shader clock the timed launches ran at, and the
+                     # fraction of the dense peak at that clock (the nameplate
+                     # figure assumes 2.4 GHz)
+                     "clock_mhz": None if g["clock_mhz"] is None else round(g["clock_mhz"], 1),
+                     "frac_at_clock": None if not g["clock_mhz"] else
+                     round(achieved / (PEAK_BF16_TFLOPS * g["clock_mhz"] / PEAK_CLOCK_MHZ), 4)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -140,9 +140,12 @@ def test_module_cache_loads_once(hiplib, rng):
 HOST_AXPY_C = r"""
 #include <stdint.h>
 typedef struct { float *alloc, *aligned; int64_t offset, size, stride; } D1;
-/* the outlined host form of vx_img_axpy */
+int64_t vx_host_worker_id(void);
+int64_t vx_host_worker_count(void);
+/* the outlined host form of vx_img_axpy: a `launch=` region, so (as the
+ * compiler emits it) each host worker takes its slice of the range */
 void _vx_ciface_vx_img_axpy(D1 *x, D1 *y, float a) {
-  for (int64_t i = 0; i < x->size; ++i)
+  for (int64_t i = vx_host_worker_id(); i < x->size; i += vx_host_worker_count())
     y->aligned[y->offset + i * y->stride] =
         a * x->aligned[x->offset + i * x->stride] + y->aligned[y->offset + i * y->stride];
 }

@@ -42,8 +42,9 @@ HIP_CTRL_GEMM_KERNEL = CTRL_VENDOR_BASE + 1
 HIP_CTRL_STATS = CTRL_VENDOR_BASE + 2
 HIP_CTRL_POOL_DRAIN = CTRL_VENDOR_BASE + 3
 HIP_CTRL_IMAGE_STATS = CTRL_VENDOR_BASE + 4
-(GEMM_AUTO, GEMM_MFMA, GEMM_TILED, GEMM_MFMA_PIPE4, GEMM_MFMA_PIPE8, GEMM_MFMA_IL, GEMM_MFMA_DMA,
- GEMM_MFMA_DMA8, GEMM_MFMA_PP, GEMM_F32_MFMA) = (0, 1, 2, 3, 4, 5, 6, 7, 8, 9)
+HIP_CTRL_CLOCK_STAMPS = CTRL_VENDOR_BASE + 5
+# Kernels the GEMM control opcode can force (0 = automatic choice).
+GEMM_AUTO, GEMM_TILED, GEMM_MFMA_PP, GEMM_F32_MFMA = 0, 2, 8, 9
 
 
 def memref_tag(dtype: int, rank: int) -> int:

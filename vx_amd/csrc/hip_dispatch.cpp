@@ -358,6 +358,22 @@ std::atomic<int64_t> stat_image_launches{0};
 std::atomic<int64_t> stat_image_loads{0};
 std::atomic<int> forced_gemm_kernel{0};
 
+/* Clock stamps of routed MFMA GEMMs (VX_HIP_CTRL_CLOCK_STAMPS): a ring of
+ * `slots` records of 4 u64 in HBM, one per launch in turn; off when null. */
+std::mutex stamps_mutex;
+uint64_t *stamps_base = nullptr;
+int64_t stamps_slots = 0, stamps_next = 0;
+
+uint64_t *next_stamp() {
+  std::lock_guard<std::mutex> hold(stamps_mutex);
+  if (!stamps_base || stamps_slots <= 0) {
+    return nullptr;
+  }
+  uint64_t *p = stamps_base + 4 * (stamps_next % stamps_slots);
+  ++stamps_next;
+  return p;
+}
+
 /* An operand on the device: used in place, or a pooled packed copy. */
 struct DeviceOperand {
   void *ptr = nullptr;
@@ -441,6 +457,7 @@ bool run_gemm(const vx_gemm_plan &plan) {
   g.m = plan.m, g.n = plan.n, g.k = plan.k;
   g.a = a.ptr, g.b = b.ptr, g.c = c.ptr;
   g.lda = a.row_stride, g.ldb = b.row_stride, g.ldc = c.row_stride;
+  g.stamp = next_stamp();
 
   vxk::GemmKernel which = vxk::gemm_pick(g);
   const int forced = forced_gemm_kernel.load();
@@ -1137,6 +1154,7 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
 #define VX_HIP_CTRL_STATS (VX_CTRL_VENDOR_BASE + 2)
 #define VX_HIP_CTRL_POOL_DRAIN (VX_CTRL_VENDOR_BASE + 3)
 #define VX_HIP_CTRL_IMAGE_STATS (VX_CTRL_VENDOR_BASE + 4)
+#define VX_HIP_CTRL_CLOCK_STAMPS (VX_CTRL_VENDOR_BASE + 5)
 
 int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   switch (opcode) {
@@ -1193,13 +1211,12 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     return 1;
   }
   case VX_HIP_CTRL_GEMM_KERNEL: {
-    /* payload -> int32_t: 0 automatic, 1 MFMA (plain), 2 tiled, 3 MFMA
-     * pipelined on 4 waves, 4 MFMA pipelined on 8 waves, 5 MFMA with the
-     * non-MFMA work interleaved, 6/7 MFMA with direct-to-LDS loads (4 or 8
-     * waves), 8 the same loads with SIMD-sharing waves taking turns on
-     * 16x16x32 MFMAs, 9 f32 on f32 MFMAs. */
+    /* payload -> int32_t: 0 automatic, 2 tiled (exact k order), 8 MFMA
+     * ping-pong (16-bit inputs), 9 f32 on f32 MFMAs. A forced kernel applies
+     * where it takes the shape. */
     const int32_t *which = static_cast<const int32_t *>(payload);
-    if (!which || *which < 0 || *which > 9) {
+    if (!which || !(*which == 0 || *which == vxk::GEMM_TILED ||
+                    *which == vxk::GEMM_MFMA_PP || *which == vxk::GEMM_F32_MFMA)) {
       return 0;
     }
     forced_gemm_kernel.store(*which);
@@ -1228,6 +1245,23 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     }
     out[0] = stat_image_launches.load();
     out[1] = stat_image_loads.load();
+    return 1;
+  }
+  case VX_HIP_CTRL_CLOCK_STAMPS: {
+    /* payload -> {uint64_t *base; int64_t slots}: routed MFMA GEMMs record
+     * their clock counters into base[4 * (launch % slots) ...] from now on
+     * (base null: stop). The ring restarts at slot 0. */
+    const struct {
+      uint64_t *base;
+      int64_t slots;
+    } *ring = static_cast<const decltype(ring)>(payload);
+    if (!ring || ring->slots < 0 || (ring->base && !is_device_ptr(ring->base))) {
+      return 0;
+    }
+    std::lock_guard<std::mutex> hold(stamps_mutex);
+    stamps_base = ring->base;
+    stamps_slots = ring->slots;
+    stamps_next = 0;
     return 1;
   }
   case VX_HIP_CTRL_POOL_DRAIN:

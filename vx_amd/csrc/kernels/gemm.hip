@@ -12,12 +12,6 @@
  * so the 32 consecutive tiles each XCD receives form a 4x8 patch of C, which
  * keeps each XCD's A and B panels in its own L2.
  *
- * Earlier variants on v_mfma_f32_32x32x16 (gemm_mfma_256, gemm_mfma_pipe
- * with 4 or 8 waves, gemm_mfma_il, gemm_mfma_dma with 4 or 8 waves) stay
- * selectable for comparison and produce bit-identical results among
- * themselves: every one issues the same MFMAs on each accumulator in the
- * same k order.
- *
  * gemm_tiled takes every supported type pair, any shape and row stride:
  * 64x64 tiles, 16-deep K stages through LDS, one multiply and one add per
  * term with contraction off, k in order: for f32 this is the same
@@ -48,31 +42,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileM = 256;
 constexpr int kTileN = 256;
-constexpr int kStageK = 64;
-constexpr int kChunks = kStageK / 8; /* 16-byte k-chunks per LDS row */
-constexpr int kThreads = 256;
 constexpr int kGroupM = 4; /* tile rows per launch-order group */
-
-/* Physical chunk of logical k-chunk `c` in LDS row `row`. A permutation of
- * 0..7 per row; 16 consecutive rows at one logical chunk land on 16 distinct
- * (row parity, chunk) pairs, so a 16-lane ds_read_b128 phase is conflict-free
- * whether the LDS is 32 or 64 banks wide. */
-__device__ __forceinline__ int swz(int row, int c) {
-  return c ^ (row & 7) ^ ((row >> 3) & 1);
-}
-
-template <bool kBf16>
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  if constexpr (kBf16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
-        0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
-        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-        0);
-  }
-}
 
 template <int kOut>
 __device__ __forceinline__ void put(void *c, int64_t at, float v) {
@@ -85,335 +55,9 @@ __device__ __forceinline__ void put(void *c, int64_t at, float v) {
   }
 }
 
-template <bool kBf16, int kOut>
-__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_256(
-    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
-  __shared__ u32x4 lds[2][2][kTileM * kChunks]; /* [stage][A|B][row*8+chunk] */
-
-  const int t = threadIdx.x;
-
-  /* Launch order -> tile. Workgroup i runs on XCD i % 8; renumber so each
-   * XCD's workgroups are consecutive, then walk tiles in groups of kGroupM
-   * tile rows so consecutive numbers share A and B panels. */
-  int id = blockIdx.x;
-  const int nwg = gridDim.x;
-  if ((nwg & 7) == 0) {
-    id = (id & 7) * (nwg >> 3) + (id >> 3);
-  }
-  const int group_size = kGroupM * tiles_n;
-  const int first_m = (id / group_size) * kGroupM;
-  const int rows_in_group = min(tiles_m - first_m, kGroupM);
-  const int in_group = id % group_size;
-  const int tm = first_m + in_group % rows_in_group;
-  const int tn = in_group / rows_in_group;
-  const int64_t m0 = (int64_t)tm * kTileM;
-  const int64_t n0 = (int64_t)tn * kTileN;
-
-  /* A stage: 8 passes of 32 rows x 8 chunks. */
-  const uint16_t *a_src = A + (m0 + (t >> 3)) * lda + (t & 7) * 8;
-  const int64_t a_pass = 32 * lda;
-  /* B stage: thread owns the 8x8 block at k-chunk kc, n-block nb. */
-  const int kc = t & 7;
-  const int nb = t >> 3;
-  const uint16_t *b_src = B + (int64_t)(kc * 8) * ldb + n0 + nb * 8;
-
-  u32x4 areg[8], breg[8];
-
-  auto fetch = [&](int step) {
-    const uint16_t *ap = a_src + (int64_t)step * kStageK;
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      areg[p] = *reinterpret_cast<const u32x4 *>(ap + p * a_pass);
-    }
-    const uint16_t *bp = b_src + (int64_t)step * kStageK * ldb;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      breg[r] = *reinterpret_cast<const u32x4 *>(bp + r * ldb);
-    }
-  };
-
-  auto stash = [&](int s) {
-    u32x4 *la = lds[s][0];
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int row = p * 32 + (t >> 3);
-      la[row * kChunks + swz(row, t & 7)] = areg[p];
-    }
-    /* 8x8 transpose: word w of row r holds columns 2w (low) and 2w+1 (high);
-     * column j's k-chunk packs rows (2q, 2q+1) into word q. */
-    u32x4 col[8];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t x = breg[2 * q][w];
-        const uint32_t y = breg[2 * q + 1][w];
-        col[2 * w][q] = (x & 0xffffu) | (y << 16);
-        col[2 * w + 1][q] = (x >> 16) | (y & 0xffff0000u);
-      }
-    }
-    u32x4 *lb = lds[s][1];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = nb * 8 + j;
-      lb[row * kChunks + swz(row, kc)] = col[j];
-    }
-  };
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc[i][j][r] = 0.0f;
-      }
-    }
-  }
-
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
-  const int lrow = lane & 31;
-  const int lk = lane >> 5;
-
-  const int steps = K / kStageK;
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int step = 0; step < steps; ++step) {
-    const int s = step & 1;
-    if (step + 1 < steps) {
-      fetch(step + 1);
-    }
-    const u32x4 *la = lds[s][0];
-    const u32x4 *lb = lds[s][1];
-#pragma unroll
-    for (int ks = 0; ks < kStageK / 16; ++ks) {
-      const int c = ks * 2 + lk;
-      u32x4 af[4], bfr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * 128 + i * 32 + lrow;
-        af[i] = la[row * kChunks + swz(row, c)];
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int row = wn * 128 + j * 32 + lrow;
-        bfr[j] = lb[row * kChunks + swz(row, c)];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[i][j] = mfma32<kBf16>(af[i], bfr[j], acc[i][j]);
-        }
-      }
-    }
-    if (step + 1 < steps) {
-      stash(s ^ 1);
-    }
-    __syncthreads();
-  }
-
-  /* 32x32 accumulator layout: lane l, element r holds row
-   * 8*(r/4) + 4*(l/32) + r%4, column l%32. */
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + wn * 128 + j * 32 + lrow;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row =
-            m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        put<kOut>(C, row * ldc + col, acc[i][j][r]);
-      }
-    }
-  }
-}
-
-/* Software-pipelined variant of the same 256x256x64 tile, for kWavesM x
- * kWavesN waves (4 = one wave per SIMD, 8 = two).
- *
- * Per stage (K step of 64) the wave walks 4 k-substeps of 16. The MFMA
- * operands of substep s+1 are read from LDS into a second register set
- * before the MFMAs of substep s issue (sched_barrier keeps that order), so
- * LDS latency hides behind MFMA work instead of stalling it. The global
- * loads of the stage after next are issued after substep 2 and land in
- * registers; they are written into the idle LDS buffer after substep 1 of
- * the following stage, leaving a whole stage for the loads to arrive. One
- * barrier per stage. B's 8-row blocks are kNB columns wide (8 for 256
- * threads, 4 for 512) so each thread owns exactly one block. */
-template <int kWavesM, int kWavesN, bool kBf16, int kOut>
-__global__ __launch_bounds__(64 * kWavesM * kWavesN, 1) void gemm_mfma_pipe(
-    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
-  constexpr int kT = 64 * kWavesM * kWavesN;
-  constexpr int kTM = kTileM / kWavesM / 32; /* 32x32 tiles per wave in m */
-  constexpr int kTN = kTileN / kWavesN / 32;
-  constexpr int kALoads = kTileM * kChunks / kT;
-  constexpr int kNB = kTileN * kChunks / kT; /* B block width: 8 or 4 */
-  static_assert(kNB == 8 || kNB == 4, "one B block per thread");
-  __shared__ u32x4 lds[2][2][kTileM * kChunks];
-
-  const int t = threadIdx.x;
-  int id = blockIdx.x;
-  const int nwg = gridDim.x;
-  if ((nwg & 7) == 0) {
-    id = (id & 7) * (nwg >> 3) + (id >> 3);
-  }
-  const int group_size = kGroupM * tiles_n;
-  const int first_m = (id / group_size) * kGroupM;
-  const int rows_in_group = min(tiles_m - first_m, kGroupM);
-  const int in_group = id % group_size;
-  const int tm = first_m + in_group % rows_in_group;
-  const int tn = in_group / rows_in_group;
-  const int64_t m0 = (int64_t)tm * kTileM;
-  const int64_t n0 = (int64_t)tn * kTileN;
-
-  const uint16_t *a_src = A + (m0 + (t >> 3)) * lda + (t & 7) * 8;
-  const int64_t a_pass = (int64_t)(kT / 8) * lda;
-  const int kc = t & 7;
-  const int nb = t >> 3;
-  const uint16_t *b_src = B + (int64_t)(kc * 8) * ldb + n0 + nb * kNB;
-
-  using BRow = typename std::conditional<kNB == 8, u32x4, u32x2>::type;
-  u32x4 areg[kALoads];
-  BRow breg[8]; /* one row of the thread's 8 x kNB block of B */
-
-  auto fetch = [&](int step) {
-    const uint16_t *ap = a_src + (int64_t)step * kStageK;
-#pragma unroll
-    for (int p = 0; p < kALoads; ++p) {
-      areg[p] = *reinterpret_cast<const u32x4 *>(ap + p * a_pass);
-    }
-    const uint16_t *bp = b_src + (int64_t)step * kStageK * ldb;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      breg[r] = *reinterpret_cast<const BRow *>(bp + r * ldb);
-    }
-  };
-
-  auto stash = [&](int s) {
-    u32x4 *la = lds[s][0];
-#pragma unroll
-    for (int p = 0; p < kALoads; ++p) {
-      const int row = p * (kT / 8) + (t >> 3);
-      la[row * kChunks + swz(row, t & 7)] = areg[p];
-    }
-    u32x4 *lb = lds[s][1];
-#pragma unroll
-    for (int w = 0; w < kNB / 2; ++w) {
-      u32x4 lo, hi;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t x = breg[2 * q][w];
-        const uint32_t y = breg[2 * q + 1][w];
-        lo[q] = (x & 0xffffu) | (y << 16);
-        hi[q] = (x >> 16) | (y & 0xffff0000u);
-      }
-      const int row = nb * kNB + 2 * w;
-      lb[row * kChunks + swz(row, kc)] = lo;
-      lb[(row + 1) * kChunks + swz(row + 1, kc)] = hi;
-    }
-  };
-
-  f32x16 acc[kTM][kTN];
-#pragma unroll
-  for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc[i][j][r] = 0.0f;
-      }
-    }
-  }
-
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int wm = wave / kWavesN;
-  const int wn = wave % kWavesN;
-  const int lrow = lane & 31;
-  const int lk = lane >> 5;
-  const int a_row0 = wm * (kTileM / kWavesM) + lrow;
-  const int b_row0 = wn * (kTileN / kWavesN) + lrow;
-
-  u32x4 fa[2][kTM], fb[2][kTN];
-  auto frags = [&](int s, int ks, u32x4 *af, u32x4 *bfr) {
-    const u32x4 *la = lds[s][0];
-    const u32x4 *lb = lds[s][1];
-    const int c = ks * 2 + lk;
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-      const int row = a_row0 + i * 32;
-      af[i] = la[row * kChunks + swz(row, c)];
-    }
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int row = b_row0 + j * 32;
-      bfr[j] = lb[row * kChunks + swz(row, c)];
-    }
-  };
-
-  const int steps = K / kStageK;
-  fetch(0);
-  stash(0);
-  if (steps > 1) {
-    fetch(1);
-  }
-  __syncthreads();
-  for (int step = 0; step < steps; ++step) {
-    const int s = step & 1;
-    frags(s, 0, fa[0], fb[0]);
-#pragma unroll
-    for (int ks = 0; ks < kStageK / 16; ++ks) {
-      if (ks + 1 < kStageK / 16) {
-        frags(s, ks + 1, fa[(ks + 1) & 1], fb[(ks + 1) & 1]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-        for (int j = 0; j < kTN; ++j) {
-          acc[i][j] = mfma32<kBf16>(fa[ks & 1][i], fb[ks & 1][j], acc[i][j]);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (ks == 1 && step + 1 < steps) {
-        stash(s ^ 1);
-      }
-      if (ks == 2 && step + 2 < steps) {
-        fetch(step + 2);
-      }
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int64_t col = n0 + wn * (kTileN / kWavesN) + j * 32 + lrow;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * (kTileM / kWavesM) + i * 32 + 8 * (r >> 2) +
-                            4 * lk + (r & 3);
-        put<kOut>(C, row * ldc + col, acc[i][j][r]);
-      }
-    }
-  }
-}
-
-/* Direct-to-LDS variant for gfx950: the same 256x256 tile and wave layout,
- * K walked in stages of 32 through a ring of kDmaStages LDS slots (32 KiB
- * each).
+/* Direct-to-LDS staging for gfx950: K is walked in stages of 32 through a
+ * ring of LDS slots (32 KiB each: a 256 x 32 plane of A and a 32 x 256 plane
+ * of B).
  *
  * Global data goes straight into LDS (buffer_load_dwordx4 ... lds): lane i of
  * a load writes the 16 bytes at LDS base + 16*i, so each lane fetches the
@@ -433,10 +77,6 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN, 1) void gemm_mfma_pipe(
  * The buffer descriptors bound each load to the operand's extent, so an
  * offset past it reads zeros instead of faulting. */
 constexpr int kDStageK = 32;
-#ifndef VX_GEMM_DMA_STAGES
-#define VX_GEMM_DMA_STAGES 4
-#endif
-constexpr int kDmaStages = VX_GEMM_DMA_STAGES; /* LDS ring depth */
 constexpr int kDUnits = kTileM * kDStageK / 8; /* 16-byte units per plane */
 constexpr int kBufferFlags = 0x00020000;       /* raw 32-bit dwords */
 
@@ -446,11 +86,6 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int dswz_a(int row, int c) {
   return c ^ (((row >> 1) ^ (row >> 2)) & 3);
-}
-
-__device__ __forceinline__ int dswz_b(int k, int c) {
-  const int q = k & 3;
-  return c ^ ((q << 1) ^ (q << 2));
 }
 
 /* Wait until at most `n` of this wave's vector memory operations are
@@ -520,180 +155,6 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void *base, int bytes) {
   return r;
 }
 
-template <int kWM, int kWN, int kNS, bool kBf16, int kOut>
-__global__ __launch_bounds__(64 * kWM * kWN, 1) void gemm_mfma_dma(
-    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
-  constexpr int kLoads = kDUnits / 64 / (kWM * kWN); /* per wave per plane */
-  constexpr int kWaveM = kTileM / kWM;                /* rows of C per wave */
-  constexpr int kWaveN = kTileN / kWN;                /* columns per wave */
-  constexpr int kTM = kWaveM / 32;
-  constexpr int kTN = kWaveN / 32;
-  static_assert(kLoads >= 1 && kTM >= 1 && kTN >= 1, "wave grid");
-  static_assert(kNS >= 3 && kNS * 2 * kDUnits * 16 <= 160 * 1024, "LDS ring");
-  __shared__ u32x4 ring[kNS][2][kDUnits];
-
-  const int t = threadIdx.x;
-  int id = blockIdx.x;
-  const int nwg = gridDim.x;
-  if ((nwg & 7) == 0) {
-    id = (id & 7) * (nwg >> 3) + (id >> 3);
-  }
-  const int group_size = kGroupM * tiles_n;
-  const int first_m = (id / group_size) * kGroupM;
-  const int rows_in_group = min(tiles_m - first_m, kGroupM);
-  const int in_group = id % group_size;
-  const int tm = first_m + in_group % rows_in_group;
-  const int tn = in_group / rows_in_group;
-  const int64_t m0 = (int64_t)tm * kTileM;
-  const int64_t n0 = (int64_t)tn * kTileN;
-
-  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int lane = t & 63;
-
-  /* Byte offsets of this lane's loads, fixed for the whole K walk: load p
-   * of this wave fills units (wave*kLoads + p)*64 + lane of each plane. */
-  uint32_t a_off[kLoads], b_off[kLoads];
-#pragma unroll
-  for (int p = 0; p < kLoads; ++p) {
-    const int u = (wave * kLoads + p) * 64 + lane;
-    const int arow = u >> 2;
-    a_off[p] = (uint32_t)(arow * lda * 2 + dswz_a(arow, u & 3) * 16);
-    const int bk = u >> 5;
-    b_off[p] = (uint32_t)(bk * ldb * 2 + dswz_b(bk, u & 31) * 16);
-  }
-  const int a_bytes = (int)((kTileM - 1) * lda * 2 + kDStageK * 2);
-  const int b_bytes = (int)((kDStageK - 1) * ldb * 2 + kTileN * 2);
-
-  const uint32_t ring_base =
-      (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
-  auto issue = [&](int step, int slot) {
-    const i32x4 ra =
-        buffer_rsrc(A + m0 * lda + (int64_t)step * kDStageK, a_bytes);
-    const i32x4 rb =
-        buffer_rsrc(B + (int64_t)step * kDStageK * ldb + n0, b_bytes);
-    const uint32_t la = ring_base + (uint32_t)(slot * 2 * kDUnits * 16) +
-                        (uint32_t)(wave * kLoads * 64 * 16);
-#pragma unroll
-    for (int p = 0; p < kLoads; ++p) {
-      dma16(ra, a_off[p], la + p * 64 * 16);
-    }
-#pragma unroll
-    for (int p = 0; p < kLoads; ++p) {
-      dma16(rb, b_off[p], la + kDUnits * 16 + p * 64 * 16);
-    }
-  };
-
-  f32x16 acc[kTM][kTN];
-#pragma unroll
-  for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc[i][j][r] = 0.0f;
-      }
-    }
-  }
-
-  const int wm = wave / kWN;
-  const int wn = wave % kWN;
-  const int lrow = lane & 31;
-  const int lk = lane >> 5;
-  /* Transposed B read: group g = lane/16, lane i of the group reads row
-   * k + i/4 at columns 4*(i%4)..+3 of its 16-column half. */
-  const int tr_k = 8 * lk + ((lane & 15) >> 2);
-  const int tr_n = wn * kWaveN + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-
-  /* MFMA operands of k-substep ks of the stage in `slot`. */
-  auto frags = [&](int slot, int ks, u32x4 (&af)[kTM], u32x4 (&bfr)[kTN]) {
-    const u32x4 *la = ring[slot][0];
-    const VX_LDS char *lb = (const VX_LDS char *)&ring[slot][1][0];
-    const int c = ks * 2 + lk;
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-      const int row = wm * kWaveM + i * 32 + lrow;
-      af[i] = la[row * 4 + dswz_a(row, c)];
-    }
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int n = tr_n + j * 32;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int k = ks * 16 + tr_k + 4 * h;
-        const int at = k * (kTileN * 2) + dswz_b(k, n >> 3) * 16 + (n & 7) * 2;
-        const u32x2 w = __builtin_bit_cast(
-            u32x2,
-            __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS i16x4 *)(lb + at)));
-        bfr[j][2 * h] = w[0];
-        bfr[j][2 * h + 1] = w[1];
-      }
-    }
-  };
-  auto mfmas = [&](const u32x4 (&af)[kTM], const u32x4 (&bfr)[kTN]) {
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-      for (int j = 0; j < kTN; ++j) {
-        acc[i][j] = mfma32<kBf16>(af[i], bfr[j], acc[i][j]);
-      }
-    }
-  };
-
-  /* Stage s lives in slot s % kNS. Entering step s, stages up to s + kNS - 2
-   * have been issued and the first substep of stage s is in registers. The
-   * step waits for stage s+1 to land (this wave's loads, then the barrier
-   * for everyone's), refills the slot stage s-1 vacated with stage s+kNS-1,
-   * and reads the first substep of stage s+1 while stage s's second substep
-   * runs on the MFMA pipe. */
-  const int steps = K / kDStageK;
-#pragma unroll
-  for (int s = 0; s < kNS - 1; ++s) {
-    if (s < steps) {
-      issue(s, s);
-    }
-  }
-  wait_stages<kNS - 2, 2 * kLoads>(min(steps - 1, kNS - 2));
-  lds_barrier();
-  u32x4 fa0[kTM], fb0[kTN], fa1[kTM], fb1[kTN];
-  frags(0, 0, fa0, fb0);
-  for (int step = 0; step < steps; ++step) {
-    if (step + 1 < steps) {
-      wait_stages<kNS - 3, 2 * kLoads>(min(steps - 2 - step, kNS - 3));
-    }
-    lds_barrier();
-    if (step + kNS - 1 < steps) {
-      issue(step + kNS - 1, (step + kNS - 1) % kNS);
-    }
-    const int slot = step % kNS;
-    frags(slot, 1, fa1, fb1);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa0, fb0);
-    __builtin_amdgcn_sched_barrier(0);
-    /* Unconditional: past the last stage this reads a stale slot nobody
-     * uses, and straight-line code lets the LDS waits stay partial. */
-    frags((step + 1) % kNS, 0, fa0, fb0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(fa1, fb1);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-#pragma unroll
-  for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int64_t col = n0 + wn * kWaveN + j * 32 + lrow;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row =
-            m0 + wm * kWaveM + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        put<kOut>(C, row * ldc + col, acc[i][j][r]);
-      }
-    }
-  }
-}
-
 /* Ping-pong variant on v_mfma_f32_16x16x32: the same 256x256 tile, the same
  * 4-slot ring of K=32 stages filled by buffer-to-LDS loads, 8 waves (2x4,
  * 128x64 of C each), and the two waves that share a SIMD take turns.
@@ -748,8 +209,18 @@ template <bool kBf16, int kOut>
 __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
     void *__restrict__ C, int64_t M, int64_t N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n) {
+    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n,
+    uint64_t *__restrict__ stamp) {
   constexpr int kNS = 4;
+  /* Optional clock stamp (null in ordinary launches; the branch is uniform):
+   * workgroup 0 records the shader-clock counter and the constant 100 MHz
+   * real-time counter at its start and end, so a caller can read the clock
+   * the kernel actually ran at. */
+  uint64_t clk0 = 0, rt0 = 0;
+  if (stamp && blockIdx.x == 0) {
+    clk0 = __builtin_amdgcn_s_memtime();
+    rt0 = __builtin_amdgcn_s_memrealtime();
+  }
   constexpr int kLoads = kDUnits / 64 / 8; /* per wave per plane */
   constexpr int kTM = 8;                   /* 16-row blocks per wave */
   constexpr int kTN = 4;                   /* 16-column blocks per wave */
@@ -905,219 +376,13 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
   if (wm == 0) {
     lds_barrier(); /* matches group 1's extra barrier before the loop */
   }
-}
-
-/* Interleaved variant: the same tile, the same LDS layout and the same MFMA
- * order (so bit-identical results), with every non-MFMA instruction of a
- * stage issued in the shadow of an MFMA. With one wave per SIMD the MFMA
- * pipe otherwise idles while the wave issues its LDS writes, B transpose,
- * global loads and address arithmetic between MFMA groups.
- *
- * A stage's body is one straight-line block (no branches: the last stages
- * re-fetch the final K step, in bounds, instead of skipping), split into its
- * four k-substeps of 16 MFMAs each. Alongside substep 0 the wave reads the
- * operands of substep 1 and writes its A staging registers into the idle LDS
- * buffer; alongside substep 1, operands of 2 and the B transpose and write;
- * alongside 2, operands of 3 and the global loads of A two stages ahead;
- * alongside 3, those of B. sched_group_barrier fixes the interleave: one
- * MFMA, then one memory instruction (plus VALU for the transpose). */
-template <bool kBf16, int kOut>
-__global__ __launch_bounds__(kThreads, 1) void gemm_mfma_il(
-    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-    void *__restrict__ C, int K, int64_t lda, int64_t ldb, int64_t ldc,
-    int tiles_m, int tiles_n) {
-  __shared__ u32x4 lds[2][2][kTileM * kChunks];
-
-  const int t = threadIdx.x;
-  int id = blockIdx.x;
-  const int nwg = gridDim.x;
-  if ((nwg & 7) == 0) {
-    id = (id & 7) * (nwg >> 3) + (id >> 3);
-  }
-  const int group_size = kGroupM * tiles_n;
-  const int first_m = (id / group_size) * kGroupM;
-  const int rows_in_group = min(tiles_m - first_m, kGroupM);
-  const int in_group = id % group_size;
-  const int tm = first_m + in_group % rows_in_group;
-  const int tn = in_group / rows_in_group;
-  const int64_t m0 = (int64_t)tm * kTileM;
-  const int64_t n0 = (int64_t)tn * kTileN;
-
-  const uint16_t *a_src = A + (m0 + (t >> 3)) * lda + (t & 7) * 8;
-  const int64_t a_pass = 32 * lda;
-  const int kc = t & 7;
-  const int nb = t >> 3;
-  const uint16_t *b_src = B + (int64_t)(kc * 8) * ldb + n0 + nb * 8;
-
-  u32x4 areg[8], breg[8];
-
-  auto fetch_a = [&](int step) {
-    const uint16_t *ap = a_src + (int64_t)step * kStageK;
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      areg[p] = *reinterpret_cast<const u32x4 *>(ap + p * a_pass);
-    }
-  };
-  auto fetch_b = [&](int step) {
-    const uint16_t *bp = b_src + (int64_t)step * kStageK * ldb;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      breg[r] = *reinterpret_cast<const u32x4 *>(bp + r * ldb);
-    }
-  };
-  auto stash_a = [&](int s) {
-    u32x4 *la = lds[s][0];
-#pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int row = p * 32 + (t >> 3);
-      la[row * kChunks + swz(row, t & 7)] = areg[p];
-    }
-  };
-  auto stash_b = [&](int s) {
-    u32x4 *lb = lds[s][1];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      u32x4 lo, hi;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t x = breg[2 * q][w];
-        const uint32_t y = breg[2 * q + 1][w];
-        lo[q] = (x & 0xffffu) | (y << 16);
-        hi[q] = (x >> 16) | (y & 0xffff0000u);
-      }
-      const int row = nb * 8 + 2 * w;
-      lb[row * kChunks + swz(row, kc)] = lo;
-      lb[(row + 1) * kChunks + swz(row + 1, kc)] = hi;
-    }
-  };
-
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        acc[i][j][r] = 0.0f;
-      }
-    }
-  }
-
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
-  const int lrow = lane & 31;
-  const int lk = lane >> 5;
-
-  u32x4 fa[2][4], fb[2][4];
-  auto frags = [&](int s, int ks, u32x4 *af, u32x4 *bfr) {
-    const u32x4 *la = lds[s][0];
-    const u32x4 *lb = lds[s][1];
-    const int c = ks * 2 + lk;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wm * 128 + i * 32 + lrow;
-      af[i] = la[row * kChunks + swz(row, c)];
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = wn * 128 + j * 32 + lrow;
-      bfr[j] = lb[row * kChunks + swz(row, c)];
-    }
-  };
-  auto mfmas = [&](const u32x4 *af, const u32x4 *bfr) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[i][j] = mfma32<kBf16>(af[i], bfr[j], acc[i][j]);
-      }
-    }
-  };
-
-  constexpr int kMfma = 0x008, kValu = 0x002, kVmemRead = 0x020,
-                kDsRead = 0x100, kDsWrite = 0x200;
-
-  const int steps = K / kStageK;
-  fetch_a(0);
-  fetch_b(0);
-  stash_a(0);
-  stash_b(0);
-  fetch_a(min(1, steps - 1));
-  fetch_b(min(1, steps - 1));
-  __syncthreads();
-  for (int step = 0; step < steps; ++step) {
-    const int s = step & 1;
-    const int ahead = min(step + 2, steps - 1);
-    frags(s, 0, fa[0], fb[0]);
-    /* substep 0: operands of 1, A into the idle buffer */
-    frags(s, 1, fa[1], fb[1]);
-    stash_a(s ^ 1);
-    mfmas(fa[0], fb[0]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
-    }
-    /* substep 1: operands of 2, B transposed into the idle buffer */
-    frags(s, 2, fa[0], fb[0]);
-    stash_b(s ^ 1);
-    mfmas(fa[1], fb[1]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kValu, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
-    }
-    /* substep 2: operands of 3, global loads of A two stages ahead */
-    frags(s, 3, fa[1], fb[1]);
-    fetch_a(ahead);
-    mfmas(fa[0], fb[0]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
-    }
-    /* substep 3: global loads of B two stages ahead */
-    fetch_b(ahead);
-    mfmas(fa[1], fb[1]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kMfma, 8, 0);
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + wn * 128 + j * 32 + lrow;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row =
-            m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        put<kOut>(C, row * ldc + col, acc[i][j][r]);
-      }
-    }
+  if (stamp && blockIdx.x == 0 && t == 0) {
+    const uint64_t clk1 = __builtin_amdgcn_s_memtime();
+    const uint64_t rt1 = __builtin_amdgcn_s_memrealtime();
+    stamp[0] = clk0;
+    stamp[1] = rt0;
+    stamp[2] = clk1;
+    stamp[3] = rt1;
   }
 }
 
@@ -1351,24 +616,6 @@ __global__ __launch_bounds__(256) void gemm_tiled(const void *__restrict__ A,
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-bool mfma_takes(const GemmArgs &g) {
-  const bool sixteen = g.in_dtype == VX_DTYPE_BF16 || g.in_dtype == VX_DTYPE_F16;
-  const bool out_ok = g.out_dtype == VX_DTYPE_F32 || g.out_dtype == g.in_dtype;
-  return sixteen && out_ok && g.m > 0 && g.n > 0 && g.k > 0 &&
-         g.m % kTileM == 0 && g.n % kTileN == 0 && g.k % kStageK == 0 &&
-         g.k <= INT32_MAX && (g.m / kTileM) * (g.n / kTileN) <= INT32_MAX &&
-         g.lda % 8 == 0 && g.ldb % 8 == 0 && g.lda >= g.k && g.ldb >= g.n &&
-         g.ldc >= g.n && aligned16(g.a) && aligned16(g.b);
-}
-
-/* The direct-to-LDS kernel addresses a tile's A panel and a stage's B rows
- * with 32-bit byte offsets from a per-stage base. */
-bool dma_takes(const GemmArgs &g) {
-  return mfma_takes(g) &&
-         (kTileM - 1) * g.lda * 2 + kDStageK * 2 <= INT32_MAX &&
-         (kDStageK - 1) * g.ldb * 2 + kTileN * 2 <= INT32_MAX;
-}
-
 /* The ping-pong kernel takes any M and any N that is a multiple of 8: edge
  * tiles read zeros past the operands' ends and store only inside C. K must
  * be whole stages of 32, and rows must start on 16-byte boundaries for the
@@ -1427,63 +674,13 @@ bool tiled_takes(const GemmArgs &g) {
 }
 
 template <bool kBf16, int kOut>
-void launch_mfma(const GemmArgs &g, hipStream_t s) {
-  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
-  hipLaunchKernelGGL((gemm_mfma_256<kBf16, kOut>), dim3(tiles_m * tiles_n),
-                     dim3(kThreads), 0, s, static_cast<const uint16_t *>(g.a),
-                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
-                     g.ldb, g.ldc, tiles_m, tiles_n);
-}
-
-template <int kWM, int kWN, bool kBf16, int kOut>
-void launch_pipe(const GemmArgs &g, hipStream_t s) {
-  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
-  hipLaunchKernelGGL((gemm_mfma_pipe<kWM, kWN, kBf16, kOut>),
-                     dim3(tiles_m * tiles_n), dim3(64 * kWM * kWN), 0, s,
-                     static_cast<const uint16_t *>(g.a),
-                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
-                     g.ldb, g.ldc, tiles_m, tiles_n);
-}
-
-template <int kWM, int kWN>
-void launch_pipe_any(const GemmArgs &g, hipStream_t s) {
-  const bool bf = g.in_dtype == VX_DTYPE_BF16;
-  if (g.out_dtype == VX_DTYPE_F32) {
-    bf ? launch_pipe<kWM, kWN, true, VX_DTYPE_F32>(g, s)
-       : launch_pipe<kWM, kWN, false, VX_DTYPE_F32>(g, s);
-  } else if (bf) {
-    launch_pipe<kWM, kWN, true, VX_DTYPE_BF16>(g, s);
-  } else {
-    launch_pipe<kWM, kWN, false, VX_DTYPE_F16>(g, s);
-  }
-}
-
-template <bool kBf16, int kOut>
-void launch_il(const GemmArgs &g, hipStream_t s) {
-  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
-  hipLaunchKernelGGL((gemm_mfma_il<kBf16, kOut>), dim3(tiles_m * tiles_n),
-                     dim3(kThreads), 0, s, static_cast<const uint16_t *>(g.a),
-                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
-                     g.ldb, g.ldc, tiles_m, tiles_n);
-}
-
-template <int kWM, int kWN, bool kBf16, int kOut>
-void launch_dma(const GemmArgs &g, hipStream_t s) {
-  const int tiles_m = (int)(g.m / kTileM), tiles_n = (int)(g.n / kTileN);
-  hipLaunchKernelGGL((gemm_mfma_dma<kWM, kWN, kDmaStages, kBf16, kOut>),
-                     dim3(tiles_m * tiles_n), dim3(64 * kWM * kWN), 0, s, static_cast<const uint16_t *>(g.a),
-                     static_cast<const uint16_t *>(g.b), g.c, (int)g.k, g.lda,
-                     g.ldb, g.ldc, tiles_m, tiles_n);
-}
-
-template <bool kBf16, int kOut>
 void launch_pp(const GemmArgs &g, hipStream_t s) {
   const int tiles_m = (int)((g.m + kTileM - 1) / kTileM);
   const int tiles_n = (int)((g.n + kTileN - 1) / kTileN);
   hipLaunchKernelGGL((gemm_mfma_pp<kBf16, kOut>), dim3(tiles_m * tiles_n),
                      dim3(512), 0, s, static_cast<const uint16_t *>(g.a),
                      static_cast<const uint16_t *>(g.b), g.c, g.m, g.n,
-                     (int)g.k, g.lda, g.ldb, g.ldc, tiles_m, tiles_n);
+                     (int)g.k, g.lda, g.ldb, g.ldc, tiles_m, tiles_n, g.stamp);
 }
 
 void launch_pp_any(const GemmArgs &g, hipStream_t s) {
@@ -1494,30 +691,6 @@ void launch_pp_any(const GemmArgs &g, hipStream_t s) {
     launch_pp<true, VX_DTYPE_BF16>(g, s);
   } else {
     launch_pp<false, VX_DTYPE_F16>(g, s);
-  }
-}
-
-template <int kWM, int kWN>
-void launch_dma_any(const GemmArgs &g, hipStream_t s) {
-  const bool bf = g.in_dtype == VX_DTYPE_BF16;
-  if (g.out_dtype == VX_DTYPE_F32) {
-    bf ? launch_dma<kWM, kWN, true, VX_DTYPE_F32>(g, s)
-       : launch_dma<kWM, kWN, false, VX_DTYPE_F32>(g, s);
-  } else if (bf) {
-    launch_dma<kWM, kWN, true, VX_DTYPE_BF16>(g, s);
-  } else {
-    launch_dma<kWM, kWN, false, VX_DTYPE_F16>(g, s);
-  }
-}
-
-void launch_il_any(const GemmArgs &g, hipStream_t s) {
-  const bool bf = g.in_dtype == VX_DTYPE_BF16;
-  if (g.out_dtype == VX_DTYPE_F32) {
-    bf ? launch_il<true, VX_DTYPE_F32>(g, s) : launch_il<false, VX_DTYPE_F32>(g, s);
-  } else if (bf) {
-    launch_il<true, VX_DTYPE_BF16>(g, s);
-  } else {
-    launch_il<false, VX_DTYPE_F16>(g, s);
   }
 }
 
@@ -1546,14 +719,6 @@ void launch_tiled(const GemmArgs &g, hipStream_t s) {
 
 bool gemm_kernel_takes(GemmKernel which, const GemmArgs &g) {
   switch (which) {
-  case GEMM_MFMA_256:
-  case GEMM_MFMA_PIPE4:
-  case GEMM_MFMA_PIPE8:
-  case GEMM_MFMA_IL:
-    return mfma_takes(g);
-  case GEMM_MFMA_DMA:
-  case GEMM_MFMA_DMA8:
-    return dma_takes(g);
   case GEMM_MFMA_PP:
     return pp_takes(g);
   case GEMM_F32_MFMA:
@@ -1578,9 +743,6 @@ GemmKernel gemm_pick(const GemmArgs &g) {
       f32_mfma_takes(g)) {
     return GEMM_F32_MFMA;
   }
-  if (mfma_takes(g)) {
-    return GEMM_MFMA_PIPE4;
-  }
   if (tiled_takes(g)) {
     return GEMM_TILED;
   }
@@ -1589,41 +751,7 @@ GemmKernel gemm_pick(const GemmArgs &g) {
 
 bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
                         hipStream_t stream) {
-  if (which == GEMM_MFMA_256) {
-    if (!mfma_takes(g)) {
-      return false;
-    }
-    const bool bf = g.in_dtype == VX_DTYPE_BF16;
-    if (g.out_dtype == VX_DTYPE_F32) {
-      bf ? launch_mfma<true, VX_DTYPE_F32>(g, stream)
-         : launch_mfma<false, VX_DTYPE_F32>(g, stream);
-    } else if (bf) {
-      launch_mfma<true, VX_DTYPE_BF16>(g, stream);
-    } else {
-      launch_mfma<false, VX_DTYPE_F16>(g, stream);
-    }
-  } else if (which == GEMM_MFMA_PIPE4 || which == GEMM_MFMA_PIPE8) {
-    if (!mfma_takes(g)) {
-      return false;
-    }
-    which == GEMM_MFMA_PIPE4 ? launch_pipe_any<2, 2>(g, stream)
-                             : launch_pipe_any<2, 4>(g, stream);
-  } else if (which == GEMM_MFMA_IL) {
-    if (!mfma_takes(g)) {
-      return false;
-    }
-    launch_il_any(g, stream);
-  } else if (which == GEMM_MFMA_DMA) {
-    if (!dma_takes(g)) {
-      return false;
-    }
-    launch_dma_any<2, 2>(g, stream);
-  } else if (which == GEMM_MFMA_DMA8) {
-    if (!dma_takes(g)) {
-      return false;
-    }
-    launch_dma_any<2, 4>(g, stream);
-  } else if (which == GEMM_MFMA_PP) {
+  if (which == GEMM_MFMA_PP) {
     if (!pp_takes(g)) {
       return false;
     }

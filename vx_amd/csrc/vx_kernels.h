@@ -25,26 +25,22 @@ struct GemmArgs {
   const void *b;
   void *c;
   int64_t lda, ldb, ldc;
+  /* Where the MFMA kernel records its clock counters (4 x u64: shader clock
+   * and real-time counter at the start and end of workgroup 0), or null. */
+  uint64_t *stamp = nullptr;
 };
 
 /* Which kernel a GEMM of this shape takes. */
 enum GemmKernel {
   GEMM_NONE = 0,
-  GEMM_MFMA_256 = 1, /* bf16/f16 MFMA 32x32x16, 256x256x64 tiles */
-  GEMM_TILED = 2,    /* any supported type, 64x64 tiles, exact k order */
-  GEMM_MFMA_PIPE4 = 3, /* as 1, software-pipelined, 4 waves */
-  GEMM_MFMA_PIPE8 = 4, /* as 1, software-pipelined, 8 waves */
-  GEMM_MFMA_IL = 5,    /* as 1, every non-MFMA instruction in MFMA shadow */
-  GEMM_MFMA_DMA = 6,   /* as 1, global -> LDS direct, 4-deep ring of K=32 */
-  GEMM_MFMA_DMA8 = 7,  /* as 6, 8 waves (two per SIMD) */
-  GEMM_MFMA_PP = 8,    /* as 7 on 16x16x32 MFMAs, SIMD-sharing waves alternate */
-  GEMM_F32_MFMA = 9,   /* f32 on 32x32x2 f32 MFMAs, 128x128 tiles */
+  GEMM_TILED = 2,   /* any supported type, 64x64 tiles, exact k order */
+  GEMM_MFMA_PP = 8, /* bf16/f16 on 16x16x32 MFMAs, 256x256 tiles, direct-to-LDS
+                       4-slot ring, the two waves of a SIMD taking turns */
+  GEMM_F32_MFMA = 9, /* f32 on 32x32x2 f32 MFMAs, 128x128 tiles */
 };
 
 inline bool gemm_is_mfma(GemmKernel k) {
-  return k == GEMM_MFMA_256 || k == GEMM_MFMA_PIPE4 || k == GEMM_MFMA_PIPE8 ||
-         k == GEMM_MFMA_IL || k == GEMM_MFMA_DMA ||
-         k == GEMM_MFMA_DMA8 || k == GEMM_MFMA_PP || k == GEMM_F32_MFMA;
+  return k == GEMM_MFMA_PP || k == GEMM_F32_MFMA;
 }
 
 GemmKernel gemm_pick(const GemmArgs &g);

@@ -130,6 +130,18 @@ class DispatchLibrary:
         if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMM_KERNEL, ctypes.byref(v)):
             raise ValueError(f"no GEMM kernel {which}")
 
+    def clock_stamps(self, base: int | None, slots: int) -> None:
+        """Have routed MFMA GEMMs record their clock counters (4 x u64 per
+        launch: shader clock and 100 MHz real-time counter at the start and
+        end of workgroup 0) into a ring of `slots` records at the HBM address
+        `base`; base None stops it."""
+        class _Ring(ctypes.Structure):
+            _fields_ = [("base", ctypes.c_void_p), ("slots", ctypes.c_int64)]
+
+        ring = _Ring(base, slots)
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_CLOCK_STAMPS, ctypes.byref(ring)):
+            raise ValueError("the library refused the clock-stamp ring")
+
     # -- memory ------------------------------------------------------------
     def transfer(self, array: np.ndarray | None, nbytes: int | None = None,
                  topo: int = abi.TOPO_GPU_BASE, space_access: int = 0) -> int:
