@@ -98,6 +98,13 @@ def test_config4_greedy_stream_matches_oracle(hiplib):
         assert list(np.argsort(-row, kind="stable")[:4]) == probe["index"][:4], f"position {pos}"
         np.testing.assert_allclose(row[probe["index"]], probe["value"], atol=2e-4,
                                    err_msg=f"position {pos}")
+    # every position: mean and spread of all 32000 logits (a wrong term
+    # anywhere in the vocabulary moves them; GPU and oracle logits differ by
+    # a few 1e-6 from summation order)
+    l64 = logits.astype(np.float64)
+    moments = np.stack([l64.mean(axis=1), l64.std(axis=1)], axis=1)
+    np.testing.assert_allclose(moments, np.array(g["logit_moments"]), atol=2e-5,
+                               err_msg="logit mean/std per position")
 
 
 def test_refusals(hiplib):

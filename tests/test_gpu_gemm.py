@@ -148,6 +148,30 @@ def test_bf16_4096_config(hiplib):
     assert abs(float(c.astype(np.float64).sum()) - sum_invariant(af, bf)) < 1e-2
 
 
+def test_bf16_8192_random(hiplib):
+    """BASELINE config 2's roofline point on random N(0, 1/64) operands (the
+    1024-workgroup grid): 16 sampled rows, spread over every XCD's share of
+    the tiles, against the oracle and against f64; the sum invariant over all
+    of C (reference scripts/tools/vx_xpu_conformance.cpp:995-1017)."""
+    announce("gemm bf16->f32 8192^3 random")
+    n = 8192
+    rng = np.random.default_rng(8192)
+    a16 = f32_to_bf16(rng.normal(0, 1 / 64, (n, n)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1 / 64, (n, n)).astype(np.float32))
+    c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, abi.DTYPE_F32)
+    assert st["gemm_mfma"] == 1
+    rows = np.array([0, 1, 255, 256, 1023, 1024, 2047, 3000, 4095, 4096, 5555, 6143, 6144,
+                     7000, 8190, 8191])
+    af, bf = bf16_to_f32(a16), bf16_to_f32(b16)
+    exact = af[rows].astype(np.float64) @ bf.astype(np.float64)
+    for i, r in enumerate(rows):
+        want = oracle.gemm_bf16_f32(a16, b16, rows=slice(int(r), int(r) + 1))[r]
+        assert_max_abs(c[r], want, BF16_ABS, f"row {r}")
+        assert_max_abs(c[r], exact[i], 1e-4, f"row {r} vs f64")
+    assert np.isfinite(c).all()
+    assert abs(float(c.astype(np.float64).sum()) - sum_invariant(af, bf)) < 5e-2
+
+
 @pytest.mark.parametrize("n", [4096, 8192])
 def test_bf16_small_integers_bit_exact(hiplib, n):
     """benchmarks/gpu_gemm inputs: every sum exact in f32, so every entry is

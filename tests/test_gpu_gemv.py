@@ -71,6 +71,77 @@ def test_ragged(hiplib, shape, batch, rng):
     assert_rel(y, oracle.gemv_i8_f64(w, s, x16), GEMV_REL, f"gemv {shape}")
 
 
+KERNEL_CASES = [
+    (abi.GEMV_ROWS, (4096, 4096), 1), (abi.GEMV_ROWS, (1000, 4112), 2),
+    (abi.GEMV_ROWS, (11008, 4096), 1), (abi.GEMV_ROWS, (4099, 11008), 1),
+    (abi.GEMV_DOT2_B4, (4096, 4096), 4), (abi.GEMV_DOT2_B4, (1001, 2064), 3),
+    (abi.GEMV_LDS, (4096, 4096), 16), (abi.GEMV_LDS, (8200, 1040), 12),
+    (abi.GEMV_LDS, (4096, 4096), 1), (abi.GEMV_LDS, (65, 272), 3),
+    (abi.GEMV_LDS, (11008, 4096), 8), (abi.GEMV_LDS, (4096, 11008), 2),
+]
+
+
+@pytest.mark.parametrize("kernel,shape,batch", KERNEL_CASES)
+def test_each_kernel(hiplib, kernel, shape, batch, rng):
+    """Each GEMV kernel forced on shapes of the config and ragged ones,
+    including shapes the automatic choice sends elsewhere, against the f64
+    oracle; nothing is written past y."""
+    announce(f"gemv kernel {kernel} {shape} batch {batch}")
+    w, s, x16 = inputs(rng, *shape, batch)
+    hiplib.force_gemv_kernel(kernel)
+    try:
+        y = run(hiplib, w, s, x16, guard=64)
+    finally:
+        hiplib.force_gemv_kernel(abi.GEMV_AUTO)
+    assert_rel(y, oracle.gemv_i8_f64(w, s, x16), GEMV_REL, f"kernel {kernel} {shape} b{batch}")
+
+
+def test_calls_back_to_back_and_in_a_graph(hiplib, rng):
+    """Calls of different shapes and kernels one after another without a host
+    wait, then the same calls replayed from a captured graph three times
+    (eager calls between replays): all match the oracle and are identical
+    from run to run."""
+    from vx_amd.runtime import HipTimer
+    announce("gemv back to back and captured")
+    shapes = [((4096, 4096), 16), ((1000, 2064), 5), ((11008, 4096), 1), ((300, 4096), 3)]
+    cases = []
+    for shape, batch in shapes:
+        w, s, x16 = inputs(rng, *shape, batch)
+        d = [DeviceArray.of(hiplib, w, abi.DTYPE_I8), DeviceArray.of(hiplib, s, abi.DTYPE_F32),
+             DeviceArray.of(hiplib, x16, abi.DTYPE_BF16),
+             DeviceArray(hiplib, (batch, shape[0]), abi.DTYPE_F32)]
+        cases.append((shape, batch, d, oracle.gemv_i8_f64(w, s, x16)))
+    t = HipTimer()
+    stream = t.stream_create()
+    hiplib.lib.vx_hip_set_stream(stream)
+    graph = None
+    try:
+        def calls():
+            for shape, batch, d, _ in cases:
+                assert gemv_i8(hiplib, d[0].ptr, d[1].ptr, d[2].ptr, d[3].ptr, *shape, batch) == 0
+
+        calls()
+        t.sync()
+        first = [d[3].numpy().copy() for _, _, d, _ in cases]
+        for (shape, batch, d, want), got in zip(cases, first):
+            assert_rel(got, want, GEMV_REL, f"eager {shape} b{batch}")
+        graph = t.capture(stream, calls)
+        for _ in range(3):
+            calls()
+            t.graph_launch(graph, stream)
+            t.sync()
+            for (shape, batch, d, want), ref in zip(cases, first):
+                assert np.array_equal(d[3].numpy(), ref), f"replay {shape} b{batch}"
+    finally:
+        hiplib.lib.vx_hip_set_stream(None)
+        if graph is not None:
+            t.graph_destroy(graph)
+        t.stream_destroy(stream)
+        for _, _, d, _ in cases:
+            for a in d:
+                a.free()
+
+
 def test_exact_integers(hiplib, rng):
     """Integer activations: every partial sum is exact in f32 whatever the
     order, so the GPU must equal scale * (exact dot) bit for bit."""

@@ -43,6 +43,9 @@ HIP_CTRL_STATS = CTRL_VENDOR_BASE + 2
 HIP_CTRL_POOL_DRAIN = CTRL_VENDOR_BASE + 3
 HIP_CTRL_IMAGE_STATS = CTRL_VENDOR_BASE + 4
 HIP_CTRL_CLOCK_STAMPS = CTRL_VENDOR_BASE + 5
+HIP_CTRL_GEMV_KERNEL = CTRL_VENDOR_BASE + 6
+# Kernels the GEMV control opcode can force (0 = automatic choice).
+GEMV_AUTO, GEMV_ROWS, GEMV_DOT2_B4, GEMV_LDS = 0, 1, 2, 3
 # Kernels the GEMM control opcode can force (0 = automatic choice).
 GEMM_AUTO, GEMM_TILED, GEMM_MFMA_PP, GEMM_F32_MFMA = 0, 2, 8, 9
 

@@ -48,6 +48,7 @@
 #include "vx_image_launch.h"
 #include "vx_kernels.h"
 #include "vx_ops_internal.h"
+#include "vx_ops_kernels.h"
 #include "vx_stream_policy.h"
 
 #include <dlfcn.h>
@@ -926,6 +927,7 @@ bool device_present() { return hip_available(); }
 bool on_device(const void *p) { return is_device_ptr(p); }
 void launched(const char *what) { started_kernel(what); }
 bool chatty() { return verbose(); }
+bool capturing() { return ::capturing(); }
 } // namespace vxops
 
 extern "C" {
@@ -1155,6 +1157,7 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
 #define VX_HIP_CTRL_POOL_DRAIN (VX_CTRL_VENDOR_BASE + 3)
 #define VX_HIP_CTRL_IMAGE_STATS (VX_CTRL_VENDOR_BASE + 4)
 #define VX_HIP_CTRL_CLOCK_STAMPS (VX_CTRL_VENDOR_BASE + 5)
+#define VX_HIP_CTRL_GEMV_KERNEL (VX_CTRL_VENDOR_BASE + 6)
 
 int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   switch (opcode) {
@@ -1262,6 +1265,18 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     stamps_base = ring->base;
     stamps_slots = ring->slots;
     stamps_next = 0;
+    return 1;
+  }
+  case VX_HIP_CTRL_GEMV_KERNEL: {
+    /* payload -> int32_t: 0 automatic, 1 one-burst dot2 rows (batch 1-2),
+     * 2 grid-stride dot2 (batch <= 4, cols <= 4096), 3 MFMA through LDS
+     * tiles. A forced kernel that does not take a shape makes the op answer
+     * VX_OP_EUNSUPP. */
+    const int32_t *which = static_cast<const int32_t *>(payload);
+    if (!which || *which < 0 || *which > 3) {
+      return 0;
+    }
+    vxk::gemv_i8_force(static_cast<vxk::GemvKernel>(*which));
     return 1;
   }
   case VX_HIP_CTRL_POOL_DRAIN:

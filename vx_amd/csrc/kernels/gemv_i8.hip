@@ -16,6 +16,7 @@
 #include "../vx_ops_kernels.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace vxk {
 namespace {
@@ -514,7 +515,30 @@ void launch_rows(const int8_t *w, const float *s, const uint16_t *x, float *y,
   }
 }
 
+std::atomic<int> forced_gemv{0};
+
+/* The automatic choice, from sweeps of every kernel over 4096 x 4096,
+ * 11008 x 4096 and 4096 x 11008: gemv_i8_rows (dot2; each workgroup one
+ * burst of loads) for batch 1 at any width and batch 2 over at most 4096
+ * columns; the grid-stride dot2 kernel, whose work per weight byte grows
+ * with the batch but overlaps the stream, for batches 3 and 4 over at most
+ * 4096 columns; otherwise the MFMA kernel, whose cost beyond the weight
+ * stream is the x operand, read once per 16 (or, for batches of 8 and more
+ * over 8192 rows and more, 64) rows. */
+GemvKernel gemv_pick(int rows, int cols, int nb) {
+  (void)rows;
+  if (nb == 1 || (nb == 2 && cols <= kGroupCols)) {
+    return GEMV_ROWS;
+  }
+  if (nb <= 4 && cols <= kGroupCols) {
+    return GEMV_DOT2_B4;
+  }
+  return GEMV_LDS;
+}
+
 } // namespace
+
+void gemv_i8_force(GemvKernel which) { forced_gemv.store((int)which); }
 
 bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
                     float *y, int64_t rows, int64_t cols, int64_t batch,
@@ -527,28 +551,40 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
     return false;
   }
   const int r = (int)rows, c = (int)cols, nb = (int)batch;
-  /* Routing, measured on 4096 x 4096, 11008 x 4096 and 4096 x 11008 with
-   * every kernel: gemv_i8_rows (dot2; each workgroup one burst of loads) for
-   * batch 1 at any width and batch 2 over at most 4096 columns; the
-   * grid-stride dot2 kernel, whose work per weight byte grows with the batch
-   * but overlaps the stream, for batches 3 and 4 over at most 4096 columns;
-   * otherwise the MFMA kernel, whose cost beyond the weight stream is the x
-   * operand, read once per 16 (or, for batches of 8 and more over 8192 rows
-   * and more, 64) rows. */
-  if (nb == 1) {
-    if (c > kGroupCols) {
-      launch_rows<1, VX_GEMV_B1_RLONG>(w, scale, x, y, r, c, nb, stream);
-    } else {
-      launch_rows<1, VX_GEMV_B1_R>(w, scale, x, y, r, c, nb, stream);
+  GemvKernel which = (GemvKernel)forced_gemv.load();
+  if (which == GEMV_AUTO) {
+    which = gemv_pick(r, c, nb);
+  }
+  switch (which) {
+  case GEMV_ROWS:
+    if (nb > 2) {
+      return false;
     }
-  } else if (nb == 2 && c <= kGroupCols) {
-    launch_rows<2, 16>(w, scale, x, y, r, c, nb, stream);
-  } else if (nb <= 4 && c <= kGroupCols) {
+    if (nb == 1) {
+      if (c > kGroupCols) {
+        launch_rows<1, VX_GEMV_B1_RLONG>(w, scale, x, y, r, c, nb, stream);
+      } else {
+        launch_rows<1, VX_GEMV_B1_R>(w, scale, x, y, r, c, nb, stream);
+      }
+    } else {
+      launch_rows<2, 16>(w, scale, x, y, r, c, nb, stream);
+    }
+    break;
+  case GEMV_DOT2_B4:
+    if (nb > 4 || c > kGroupCols) {
+      return false;
+    }
     launch_b4(w, scale, x, y, r, c, nb, stream);
-  } else if (nb >= 8 && r >= 8192) {
-    launch_lds<4>(w, scale, x, y, r, c, nb, stream);
-  } else {
-    launch_lds<1>(w, scale, x, y, r, c, nb, stream);
+    break;
+  case GEMV_LDS:
+    if (nb >= 8 && r >= 8192) {
+      launch_lds<4>(w, scale, x, y, r, c, nb, stream);
+    } else {
+      launch_lds<1>(w, scale, x, y, r, c, nb, stream);
+    }
+    break;
+  default:
+    return false;
   }
   VX_HIP_CHECK(hipGetLastError());
   return true;

@@ -58,7 +58,9 @@ int32_t vx_nn_gemv_i8_bf16(const int8_t *w, const float *scale,
   }
   if (!vxk::gemv_i8_launch(w, scale, x, y, rows, cols, batch,
                            vxops::stream())) {
-    return refuse(VX_OP_EUNSUPP, op, "w and x must be 16-byte aligned");
+    return refuse(VX_OP_EUNSUPP, op,
+                  "w and x must be 16-byte aligned (or a forced kernel does "
+                  "not take this shape)");
   }
   vxops::launched(op);
   return VX_OP_OK;

@@ -14,6 +14,8 @@ bool device_present();
 bool on_device(const void *p);
 void launched(const char *what);
 bool chatty();
+/* Whether the caller stream is capturing a hipGraph now. */
+bool capturing();
 } // namespace vxops
 
 #endif /* VX_AMD_OPS_INTERNAL_H */

@@ -16,8 +16,20 @@ namespace vxk {
  * of x) are 31-bit byte counts. */
 constexpr int64_t kGemvMaxCols = int64_t(1) << 24;
 
+/* The GEMV kernels; GEMV_AUTO picks by shape. */
+enum GemvKernel {
+  GEMV_AUTO = 0,
+  GEMV_ROWS = 1,    /* one-burst row groups on v_dot2 (batch 1 and 2) */
+  GEMV_DOT2_B4 = 2, /* grid-stride v_dot2 (batch up to 4, cols <= 4096) */
+  GEMV_LDS = 3,     /* MFMA through per-wave LDS tiles, x from L2 */
+};
+
+/* Force one kernel (GEMV_AUTO: the automatic choice again). */
+void gemv_i8_force(GemvKernel which);
+
 /* y[b, r] = scale[r] * sum_c w[r, c] * x[b, c]; cols % 16 == 0 and at most
- * kGemvMaxCols, batch 1..16, w and x 16-byte aligned. */
+ * kGemvMaxCols, batch 1..16, w and x 16-byte aligned. False (nothing
+ * launched) for a shape or alignment the chosen kernel does not take. */
 bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
                     float *y, int64_t rows, int64_t cols, int64_t batch,
                     hipStream_t stream);

@@ -130,6 +130,11 @@ class DispatchLibrary:
         if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMM_KERNEL, ctypes.byref(v)):
             raise ValueError(f"no GEMM kernel {which}")
 
+    def force_gemv_kernel(self, which: int) -> None:
+        v = ctypes.c_int32(which)
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMV_KERNEL, ctypes.byref(v)):
+            raise ValueError(f"no GEMV kernel {which}")
+
     def clock_stamps(self, base: int | None, slots: int) -> None:
         """Have routed MFMA GEMMs record their clock counters (4 x u64 per
         launch: shader clock and 100 MHz real-time counter at the start and
