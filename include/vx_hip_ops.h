@@ -182,6 +182,23 @@ int32_t vx_llama_i8_save(const char *path, const vx_llama_i8_config *cfg,
 int32_t vx_hip_image_param_count(const void *image, size_t image_size,
                                  const char *kernel);
 
+/* ---- a routed GEMM that allocates nothing -----------------------------
+ *
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory (tight serving loops, harnesses that forbid hipMalloc): the
+ * kind=matmul dispatch of vx_plugin_dispatch_async, with the same payload,
+ * arguments and result, except that host operands and a host result buffer
+ * are staged through a fixed 16 MiB array per GPU (in this library's code
+ * object) instead of the staging pool. Returns 1 when the GEMM was issued,
+ * 0 (reason on stderr, nothing launched) for a region that is not a routed
+ * GEMM, a result published through a slot (host memory the program frees),
+ * or staging beyond 16 MiB. Operands already in GPU memory need no staging.
+ * Calls on one GPU share its array: calls that overlap in time race. */
+uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
+                                       size_t payload_size, void **device_args,
+                                       const int32_t *arg_tags,
+                                       int64_t num_args);
+
 #ifdef __cplusplus
 }
 #endif

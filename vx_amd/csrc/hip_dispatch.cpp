@@ -375,6 +375,21 @@ uint64_t *next_stamp() {
   return p;
 }
 
+/* Where host operands and host results are staged: the pool, or (for
+ * vx_hip_dispatch_async_noalloc) a region handed out front to back. */
+struct Arena {
+  unsigned char *base = nullptr; /* null: the pool */
+  size_t size = 0, used = 0;
+  void *take(size_t bytes) {
+    const size_t at = (used + 255) / 256 * 256;
+    if (at > size || bytes > size - at) {
+      return nullptr;
+    }
+    used = at + bytes;
+    return base + at;
+  }
+};
+
 /* An operand on the device: used in place, or a pooled packed copy. */
 struct DeviceOperand {
   void *ptr = nullptr;
@@ -391,7 +406,7 @@ struct DeviceOperand {
 };
 
 void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
-           size_t esz, DeviceOperand &out) {
+           size_t esz, DeviceOperand &out, Arena *arena) {
   if (is_device_ptr(data)) {
     out.ptr = const_cast<void *>(data);
     out.row_stride = row_stride;
@@ -402,7 +417,7 @@ void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
   }
   const size_t width = (size_t)cols * esz;
   out.bytes = (size_t)rows * width;
-  out.ptr = pool().acquire(out.bytes);
+  out.ptr = arena ? arena->take(out.bytes) : pool().acquire(out.bytes);
   if (!out.ptr) {
     fprintf(stderr,
             "[Vx HIP] FATAL: out of device memory staging %zu bytes "
@@ -410,7 +425,7 @@ void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
             out.bytes, (long long)rows, (long long)cols);
     abort();
   }
-  out.pooled = true;
+  out.pooled = arena == nullptr;
   out.row_stride = cols;
   stat_staged_bytes += (int64_t)out.bytes;
   VX_HIP_CHECK(hipMemcpy2DAsync(out.ptr, width, data, (size_t)row_stride * esz,
@@ -418,7 +433,7 @@ void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
                                 caller_stream));
 }
 
-bool run_gemm(const vx_gemm_plan &plan) {
+bool run_gemm(const vx_gemm_plan &plan, Arena *arena = nullptr) {
   const size_t in_esz = vx_dtype_bytes(plan.dtype);
   const size_t out_esz = vx_dtype_bytes(plan.out_dtype);
   if (!in_esz || !out_esz) {
@@ -432,8 +447,8 @@ bool run_gemm(const vx_gemm_plan &plan) {
   }
 
   DeviceOperand a, b, c;
-  stage(plan.a_data, plan.m, plan.k, plan.a_row_stride, in_esz, a);
-  stage(plan.b_data, plan.k, plan.n, plan.b_row_stride, in_esz, b);
+  stage(plan.a_data, plan.m, plan.k, plan.a_row_stride, in_esz, a, arena);
+  stage(plan.b_data, plan.k, plan.n, plan.b_row_stride, in_esz, b, arena);
   const bool out_is_device =
       plan.out_kind == VX_GEMM_OUT_BUFFER && is_device_ptr(plan.out_data);
   if (out_is_device) {
@@ -441,14 +456,14 @@ bool run_gemm(const vx_gemm_plan &plan) {
     c.row_stride = plan.out_row_stride;
   } else {
     c.bytes = (size_t)plan.m * (size_t)plan.n * out_esz;
-    c.ptr = pool().acquire(c.bytes);
+    c.ptr = arena ? arena->take(c.bytes) : pool().acquire(c.bytes);
     if (!c.ptr) {
       fprintf(stderr, "[Vx HIP] FATAL: out of device memory for a %lldx%lld "
                       "GEMM result\n",
               (long long)plan.m, (long long)plan.n);
       abort();
     }
-    c.pooled = true;
+    c.pooled = arena == nullptr;
     c.row_stride = plan.n;
   }
 
@@ -918,6 +933,45 @@ void one_rank_copy(const void *in, void *out, int64_t count, size_t esz,
   }
 }
 
+/* Staging of vx_hip_dispatch_async_noalloc: a fixed array in each device's
+ * copy of this library's code object, allocated when the code object loads
+ * and held until the process ends. Host code reaches it only through the
+ * address hipGetSymbolAddress gives for the current device (the array's
+ * name is a host-side stand-in, not a device address). */
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex scratch_mutex;
+std::map<int, unsigned char *> &scratch_ptrs() {
+  static auto *m = new std::map<int, unsigned char *>();
+  return *m;
+}
+
+/* This device's scratch, looked up once per device with that device
+ * current; null (message printed) when the lookup fails. */
+unsigned char *noalloc_scratch() {
+  int device = 0;
+  VX_HIP_CHECK(hipGetDevice(&device));
+  std::lock_guard<std::mutex> hold(scratch_mutex);
+  auto found = scratch_ptrs().find(device);
+  if (found != scratch_ptrs().end()) {
+    return found->second;
+  }
+  void *ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr) {
+    (void)hipGetLastError();
+    fprintf(stderr,
+            "[Vx HIP] vx_hip_dispatch_async_noalloc: no scratch address on "
+            "GPU %d: %s\n",
+            device, hipGetErrorString(e));
+    return nullptr;
+  }
+  unsigned char *p = static_cast<unsigned char *>(ptr);
+  scratch_ptrs()[device] = p;
+  return p;
+}
+
 } // namespace
 
 /* Used by the library ops (ops.cpp). */
@@ -1010,6 +1064,76 @@ uint64_t vx_plugin_dispatch_async(const void *binary_payload,
   return 1;
 }
 
+/* The kind=matmul dispatch without allocating: host operands and a host
+ * result buffer are staged through this device's fixed scratch instead of
+ * the pool. Everything else the ABI entry point would do that allocates is
+ * refused (returns 0 with the reason on stderr, nothing launched): regions
+ * that are not a routed GEMM, results published through a slot (the
+ * program frees those with free()), and staging beyond the scratch. Calls
+ * on one GPU share its scratch: calls that overlap in time (other streams,
+ * other threads) race. */
+uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
+                                       size_t payload_size, void **device_args,
+                                       const int32_t *arg_tags,
+                                       int64_t num_args) {
+  static const char op[] = "vx_hip_dispatch_async_noalloc";
+  const int32_t abi = vx_payload_abi(binary_payload, payload_size);
+  if (abi > VX_PAYLOAD_ABI) {
+    fprintf(stderr, "[Vx HIP] %s: payload format abi=%d is newer than %d\n",
+            op, abi, VX_PAYLOAD_ABI);
+    return 0;
+  }
+  vx_gemm_plan plan;
+  if (!hip_available() ||
+      !vx_gemm_plan_decode(binary_payload, payload_size, device_args, arg_tags,
+                           num_args, &plan)) {
+    fprintf(stderr, "[Vx HIP] %s: %s is not a routed GEMM on a GPU\n", op,
+            static_cast<const char *>(binary_payload));
+    return 0;
+  }
+  if (plan.out_kind != VX_GEMM_OUT_BUFFER) {
+    fprintf(stderr,
+            "[Vx HIP] %s: a result published through a slot is host memory "
+            "this entry point would have to allocate\n",
+            op);
+    return 0;
+  }
+  select_device(vx_payload_topology(binary_payload, payload_size), "dispatch");
+  const size_t in_esz = vx_dtype_bytes(plan.dtype);
+  const size_t out_esz = vx_dtype_bytes(plan.out_dtype);
+  auto rounded = [](uint64_t b) { return (b + 255) / 256 * 256; };
+  uint64_t need = 0;
+  if (!is_device_ptr(plan.a_data)) {
+    need += rounded((uint64_t)plan.m * (uint64_t)plan.k * in_esz);
+  }
+  if (!is_device_ptr(plan.b_data)) {
+    need += rounded((uint64_t)plan.k * (uint64_t)plan.n * in_esz);
+  }
+  if (!is_device_ptr(plan.out_data)) {
+    need += rounded((uint64_t)plan.m * (uint64_t)plan.n * out_esz);
+  }
+  if (need > kNoAllocScratchBytes) {
+    fprintf(stderr,
+            "[Vx HIP] %s: staging this GEMM's host operands takes %llu bytes; "
+            "the scratch holds %zu\n",
+            op, (unsigned long long)need, kNoAllocScratchBytes);
+    return 0;
+  }
+  Arena arena;
+  if (need) {
+    arena.base = noalloc_scratch();
+    if (!arena.base) {
+      return 0;
+    }
+    arena.size = kNoAllocScratchBytes;
+  }
+  if (!run_gemm(plan, need ? &arena : nullptr)) {
+    fprintf(stderr, "[Vx HIP] %s: no GPU kernel takes this GEMM's types\n", op);
+    return 0;
+  }
+  return 1;
+}
+
 uint64_t vx_plugin_dispatch_async_flat(float *xout, float *x, float *w, int n,
                                        int d) {
   if (n <= 0 || d <= 0) {
@@ -1029,8 +1153,8 @@ uint64_t vx_plugin_dispatch_async_flat(float *xout, float *x, float *w, int n,
   }
   /* xout[d] = W[d,n] x[n] is a GEMM with m = d, k = n, N = 1. */
   DeviceOperand dw, dx, dy;
-  stage(w, d, n, n, sizeof(float), dw);
-  stage(x, n, 1, 1, sizeof(float), dx);
+  stage(w, d, n, n, sizeof(float), dw, nullptr);
+  stage(x, n, 1, 1, sizeof(float), dx, nullptr);
   const bool out_is_device = is_device_ptr(xout);
   if (out_is_device) {
     dy.ptr = xout;

@@ -73,6 +73,7 @@ HIP_SIGNATURES = {
     "vx_llama_i8_host_free": (None, [_vp]),
     "vx_llama_i8_save": (_i32, [ctypes.c_char_p, _vp, _vp]),
     "vx_hip_image_param_count": (_i32, [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_char_p]),
+    "vx_hip_dispatch_async_noalloc": (_u64, [_vp, _c_size, _vp, _vp, _i64]),
 }
 
 
