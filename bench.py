@@ -58,6 +58,18 @@ def traffic_from_profiles(name: str):
     return None
 
 
+def gemv_traffic_from_profiles() -> dict:
+    """HBM bytes per GEMV launch keyed "<rows>x<cols>_b<batch>", from
+    profiles/gemv_i8_traffic.json (rocprofv3 PMC counters); empty when not
+    measured."""
+    p = ROOT / "profiles" / "gemv_i8_traffic.json"
+    try:
+        cases = json.loads(p.read_text())["cases"]
+        return {k: v["bytes_per_launch"] for k, v in cases.items()}
+    except (ValueError, OSError, KeyError, TypeError):
+        return {}
+
+
 SETTLE_MS = 200.0  # untimed GPU work before each kernel's warmup steps
 
 
@@ -134,16 +146,25 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     # 100 MHz real-time counters at its start and end), one slot per step.
     stamps = lib.transfer(None, 32 * steps)
     lib.clock_stamps(stamps, steps)
-    events = [timer.event() for _ in range(steps + 1)]
+    e0, e1 = timer.event(), timer.event()
     t0 = time.perf_counter()
+    timer.record(e0)
+    for i in range(steps):
+        dispatch(buf, len(pl), argv, tags, nargs)
+    timer.record(e1)
+    ms_events = timer.elapsed_ms(e0, e1)
+    timer.sync()
+    wall = time.perf_counter() - t0
+    lib.clock_stamps(None, 0)
+    # The spread: the same steps again, each bracketed by its own events (an
+    # event between two launches can delay the second, so these do not
+    # enter `ms_per_step`).
+    events = [timer.event() for _ in range(steps + 1)]
     timer.record(events[0])
     for i in range(steps):
         dispatch(buf, len(pl), argv, tags, nargs)
         timer.record(events[i + 1])
-    ms_events = timer.elapsed_ms(events[0], events[-1])
     timer.sync()
-    wall = time.perf_counter() - t0
-    lib.clock_stamps(None, 0)
     step_ms = [timer.elapsed_ms(events[i], events[i + 1]) for i in range(steps)]
     st = np.empty((steps, 4), np.uint64)
     lib.fetch(stamps, st)
@@ -152,7 +173,7 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     rt = (st[:, 3] - st[:, 1]).astype(np.float64)
     clock_mhz = float(clk.sum() / rt.sum() * 100.0) if rt.sum() > 0 else None
     after = lib.stats()
-    assert after["gemm_mfma"] - before["gemm_mfma"] == steps + warmup + settled[0], \
+    assert after["gemm_mfma"] - before["gemm_mfma"] == 2 * steps + warmup + settled[0], \
         "GEMM did not take the MFMA path"
     c = dc.numpy()
     assert np.isfinite(c).all()
@@ -319,6 +340,7 @@ def bench_gemv(lib, timer, steps: int, warmup: int):
     from vx_amd.runtime import DeviceArray, gemv_i8
 
     out = []
+    gemv_traffic = gemv_traffic_from_profiles()
     rng = np.random.default_rng(11)
     stream = timer.stream_create()
     lib.lib.vx_hip_set_stream(stream)
@@ -365,7 +387,11 @@ def bench_gemv(lib, timer, steps: int, warmup: int):
                 gbs = nbytes / (us * 1e-6) / 1e9
                 out.append(dict(shape=[rows, cols], batch=batch, us=us, gbs=gbs,
                                 frac_of_hbm=gbs / PEAK_HBM_GBS, us_eager=us_eager,
-                                runs_us=spread(per_rep), rotated_copies=copies))
+                                runs_us=spread(per_rep), rotated_copies=copies,
+                                roofline={"bound": "hbm", "achieved": round(gbs, 1),
+                                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                          "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                          "traffic": gemv_traffic.get(f"{rows}x{cols}_b{batch}")}))
                 x.free()
                 y.free()
             for a in ws + [sc]:
