@@ -180,6 +180,13 @@ enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4 };
 #ifndef VX_DEC_LOGIT_PAIRS
 #define VX_DEC_LOGIT_PAIRS 4
 #endif
+/* Key and value rows each lane of step_attention_rows requests per round
+ * (two rounds in flight). Measured at config 4, graph mode: 4 and 2 about
+ * 3% faster than 8, whose first round fetches 64 KiB per workgroup before
+ * the position is known (four times what the bench's positions need). */
+#ifndef VX_ATTN_CHUNK
+#define VX_ATTN_CHUNK 4
+#endif
 template <int kMode> constexpr int pairs_per_wave() {
   return kMode == 3 ? VX_DEC_LOGIT_PAIRS : 1;
 }
@@ -694,16 +701,17 @@ template <int kL> __device__ __forceinline__ float slot_sum(float v) {
  * registers: the kL lanes that score a position also hold that position's
  * value row (the same float4 slice of it), so the probability never leaves
  * them. Wave w takes the split's local rows w * 64/kL + slot + c * 256/kL
- * (c < 8), keys and values requested together; rounds of 8 rows per lane
- * repeat with the usual online rescale while positions remain. The four
- * waves' (max, sum, weighted values) then meet once in LDS. */
+ * (c < kChunk) of each round, keys and values requested together; rounds
+ * repeat with the usual online rescale while positions remain, the next
+ * round's rows in flight while one is scored. The four waves' (max, sum,
+ * weighted values) then meet once in LDS. */
 template <int kL>
 __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int kE = 4;
   constexpr int hs = kE * kL;
   constexpr int kPerWave = 64 / kL;       /* positions a wave scores at once */
-  constexpr int kChunk = 8;               /* rows per lane in flight */
+  constexpr int kChunk = VX_ATTN_CHUNK;   /* rows per lane in flight */
   constexpr int kStride = 4 * kPerWave;   /* local rows between a wave's rows */
   constexpr int kRound = kStride * kChunk; /* local rows per round */
   __shared__ float wo[4][hs];
@@ -752,10 +760,16 @@ __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) 
   const u32x4 qw = __builtin_amdgcn_raw_buffer_load_b128(
       qrs, (int)((h * hs + sub * kE) * 4), 0, 0);
   const int ms = (a.seq_len - sp + kAttnSplit - 1) / kAttnSplit;
-  u32x4 kw[kChunk], vw[kChunk];
-  load_rows(0, ms, kw, vw);
+  /* Two rounds of rows in flight: round r + 1 is requested before round r
+   * is scored, so a long cache costs one memory round trip per two rounds
+   * rather than one per round. The first round does not depend on the
+   * position; the second is requested as soon as the position is known
+   * (all of it past n, so no memory traffic, when one round covers n). */
+  u32x4 kw0[kChunk], vw0[kChunk], kw1[kChunk], vw1[kChunk];
+  load_rows(0, ms, kw0, vw0);
   const int pos = *a.pos;
   const int n = pos >= sp ? (pos - sp) / kAttnSplit + 1 : 0;
+  load_rows(kRound, n, kw1, vw1);
   const float root = sqrtf((float)hs);
   float q[kE];
 #pragma unroll
@@ -767,7 +781,9 @@ __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) 
   for (int e = 0; e < kE; ++e) {
     acc[e] = 0.0f;
   }
-  for (int r0 = 0;; r0 += kRound) {
+  /* Scores of round r0's rows, then the online-softmax update of this
+   * wave's max, sum and weighted values. */
+  auto score_round = [&](int r0, const u32x4 (&kw)[kChunk], const u32x4 (&vw)[kChunk]) {
     float sc[kChunk];
     float mr = -INFINITY;
 #pragma unroll
@@ -809,10 +825,18 @@ __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) 
       l_run = l_run * alpha + ps;
       m_run = mnew;
     }
+  };
+  for (int r0 = 0;; r0 += 2 * kRound) {
+    score_round(r0, kw0, vw0);
     if (r0 + kRound >= n) {
       break;
     }
-    load_rows(r0 + kRound, n, kw, vw);
+    load_rows(r0 + 2 * kRound, n, kw0, vw0);
+    score_round(r0 + kRound, kw1, vw1);
+    if (r0 + 2 * kRound >= n) {
+      break;
+    }
+    load_rows(r0 + 3 * kRound, n, kw1, vw1);
   }
   /* Every lane of a slot holds that slot's sums: add the slots. */
   l_run = slot_sum<kL>(l_run);
