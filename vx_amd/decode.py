@@ -178,3 +178,43 @@ def bench(lib, timer, n_prompt: int = 16, n_steps: int = 256, reps: int = 3) -> 
                 weight_bytes_per_position=wbytes,
                 weight_gbs=wbytes * positions / best / 1e9,
                 first_tokens=[int(t) for t in toks[:8]])
+
+
+def main(argv=None) -> int:
+    """Generate from the BASELINE config-4 model (random N(0, 0.02) weights,
+    seed 0; 16-token prompt, seed 1) and print tokens per second: the
+    program a kernel trace of the decode step profiles.
+
+        python -m vx_amd.decode [--steps N] [--eager] [--lib PATH]
+    """
+    import argparse
+
+    from .runtime import DispatchLibrary, LIB_PATH
+
+    ap = argparse.ArgumentParser(description=main.__doc__.splitlines()[0])
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step's kernels one by one instead of replaying a hipGraph")
+    ap.add_argument("--lib", default=str(LIB_PATH))
+    ns = ap.parse_args(argv)
+    lib = DispatchLibrary(ns.lib)
+    cfg = CONFIG_DECODE
+    model = LlamaI8(lib, cfg, make_model(cfg, seed=0))
+    try:
+        prompt = make_prompt(cfg, n=16, seed=1)
+        model.generate(prompt, 4, graph=not ns.eager)  # warm
+        t0 = time.perf_counter()
+        toks, _ = model.generate(prompt, ns.steps, graph=not ns.eager)
+        dt = time.perf_counter() - t0
+    finally:
+        model.close()
+    mode = "eager" if ns.eager else "graph"
+    print(f"{ns.steps} tokens ({mode}) in {dt * 1e3:.2f} ms: {ns.steps / dt:.0f} tok/s; "
+          f"first tokens {[int(t) for t in toks[:8]]}", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    import sys
+
+    sys.exit(main())
