@@ -484,13 +484,16 @@ def main() -> int:
         log("gemv " + ", ".join(f"{r['shape'][0]}x{r['shape'][1]}b{r['batch']}:{r['gbs']:.0f}GB/s"
                                 for r in extra["gemv_i8"]))
     if "decode" in only:
-        try:
-            from vx_amd import decode as _decode  # noqa: F401
-        except ImportError:
-            pass
-        else:
-            log("int8 decode config 4")
-            extra["decode_i8"] = _decode.bench(lib, timer)
+        from vx_amd import decode as _decode
+
+        log("int8 decode config 4")
+        dec = _decode.bench(lib, timer)
+        # the step's algorithmic bytes (int8 weights, scales, norms, the KV
+        # rows it reads and writes) over the whole generate call's time
+        dec["roofline"] = {"bound": "hbm", "achieved": round(dec["bytes_gbs"], 1),
+                           "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(dec["bytes_gbs"] / PEAK_HBM_GBS, 4), "traffic": None}
+        extra["decode_i8"] = dec
 
     if "gemm" in only:
         log("gemm bf16->f32 8192^3 (roofline point)")

@@ -169,6 +169,8 @@ def bench(lib, timer, n_prompt: int = 16, n_steps: int = 256, reps: int = 3) -> 
     best = min(graph_best, eager_best)
     positions = n_prompt + n_steps - 1
     wbytes = cfg.int8_weight_bytes()
+    kv_total = sum(cfg.kv_bytes(p) for p in range(positions))
+    step_bytes = wbytes * positions + kv_total
     return dict(config="dim 768, 12 layers, int8 weights, bs=1, 16-token prompt + 256 greedy tokens",
                 tok_per_s=n_steps / best, positions_per_s=positions / best,
                 ms_per_position=best / positions * 1e3,
@@ -177,6 +179,8 @@ def bench(lib, timer, n_prompt: int = 16, n_steps: int = 256, reps: int = 3) -> 
                 tok_per_s_eager=n_steps / eager_best, runs_eager_s=eager,
                 weight_bytes_per_position=wbytes,
                 weight_gbs=wbytes * positions / best / 1e9,
+                kv_bytes_per_position=kv_total / positions,
+                bytes_gbs=step_bytes / best / 1e9,
                 first_tokens=[int(t) for t in toks[:8]])
 
 

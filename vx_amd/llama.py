@@ -49,6 +49,11 @@ class LlamaConfig:
         norms = 4 * (L * 2 * d + d)
         return L * per_layer + self.vocab_size * d + scales + norms
 
+    def kv_bytes(self, pos: int) -> int:
+        """KV-cache bytes the step at position `pos` moves: every layer reads
+        the f32 key and value rows 0..pos and writes row pos of each."""
+        return self.n_layers * 2 * self.kv_dim * 4 * (pos + 2)
+
 
 # BASELINE config 4: dim 768, 12 layers, 12 heads, SwiGLU 2048, vocab 32000.
 CONFIG_DECODE = LlamaConfig()
