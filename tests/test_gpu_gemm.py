@@ -264,12 +264,12 @@ def test_mfma_and_tiled_agree(hiplib, rng):
     assert_max_abs(c1, c2, 1e-3, "mfma vs tiled")
 
 
-@pytest.mark.parametrize("k", [64, 128, 192, 768])
+@pytest.mark.parametrize("k", [32, 64, 96, 128, 192, 768])
 @pytest.mark.parametrize("out_dt", [abi.DTYPE_F32, abi.DTYPE_BF16])
 def test_mfma_pp_against_oracle(hiplib, k, out_dt, rng):
     """The ping-pong kernel adds 32-term MFMA sums in k order: it is held to
-    the oracle and to f64 at K of 2, 4 and 6 stages (the ring's prologue and
-    tail cases) and 24, and it is deterministic across calls."""
+    the oracle and to f64 at K of 1, 2, 3, 4 and 6 stages (the ring's
+    prologue and tail cases) and 24, and it is deterministic across calls."""
     announce(f"gemm mfma ping-pong k={k} out={out_dt}")
     a16 = f32_to_bf16(rng.normal(0, 1, (512, k)).astype(np.float32))
     b16 = f32_to_bf16(rng.normal(0, 1, (k, 768)).astype(np.float32))
