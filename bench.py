@@ -455,8 +455,8 @@ def main() -> int:
     if ns.copy_probe:
         return copy_probe()
     if ns.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (its sharding is a "
-              "design in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (how it would "
+              "shard is a design only). Run with --gpus 1.", file=sys.stderr)
         return 2
     only = set(ns.only.split(","))
 
