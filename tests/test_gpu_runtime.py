@@ -188,6 +188,54 @@ def test_stream_ordered_memory(hiplib, rng):
         t.stream_destroy(s)
 
 
+def test_concurrent_dispatch_from_threads(hiplib):
+    """Dispatch from several threads at once, as tasks do (reference
+    runtime/cuda_dispatch.cpp:1387-1390 keeps the library's caches behind
+    mutexes; the caller stream is per thread, :205-207): four threads each
+    run f32 GEMMs with host operands and a host result (staged through the
+    shared pool), and with HBM operands, allocating, reading back and freeing
+    as they go. The exact-order kernel takes these sizes, so every result is
+    bit-equal to the oracle's."""
+    import threading
+
+    announce("dispatch from four threads at once")
+    errors = []
+
+    def work(tid):
+        rng = np.random.default_rng(100 + tid)
+        try:
+            for it in range(8):
+                n = 96 + 32 * ((tid + it) % 4)
+                a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+                b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+                want = oracle.gemm_f32(a, b)
+                c = np.full((n, n), np.nan, np.float32)
+                matmul(hiplib, abi.Descriptor(a.ctypes.data, a.shape), abi.DTYPE_F32,
+                       abi.Descriptor(b.ctypes.data, b.shape), abi.DTYPE_F32,
+                       abi.Descriptor(c.ctypes.data, c.shape), abi.DTYPE_F32)
+                if not np.array_equal(c, want):
+                    errors.append((tid, it, "host operands"))
+                da = DeviceArray.of(hiplib, a, abi.DTYPE_F32)
+                db = DeviceArray.of(hiplib, b, abi.DTYPE_F32)
+                dc = DeviceArray(hiplib, (n, n), abi.DTYPE_F32)
+                matmul(hiplib, da.descriptor(), abi.DTYPE_F32, db.descriptor(), abi.DTYPE_F32,
+                       dc.descriptor(), abi.DTYPE_F32)
+                if not np.array_equal(dc.numpy(), want):
+                    errors.append((tid, it, "HBM operands"))
+                for x in (da, db, dc):
+                    x.free()
+        except Exception as e:  # reported below, with the thread that raised it
+            errors.append((tid, -1, repr(e)))
+
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=90)
+    assert not any(t.is_alive() for t in threads), "a dispatching thread did not finish"
+    assert not errors, errors
+
+
 REFUSE = r"""
 import sys
 sys.path.insert(0, {root!r})
