@@ -140,3 +140,20 @@ def test_huge_vxq8_header_is_refused_before_allocating(lib, tmp_path):
     with pytest.raises(OSError) as e:
         read_model(lib, tmp_path / "huge.q8")
     assert e.value.args[0] == -1  # VX_OP_EINVAL: size disagrees with header
+
+
+@pytest.mark.parametrize("cfg", [llama.CONFIG_TINY,
+                                 llama.LlamaConfig(dim=96, hidden_dim=160, n_layers=3, n_heads=6,
+                                                   n_kv_heads=2, vocab_size=300, seq_len=40)])
+def test_step_byte_counts(cfg):
+    """The bytes the decode roofline divides by: int8_weight_bytes() is every
+    array of the uploaded model except the rotary table (int8 matrices, f32
+    row scales, f32 RMSNorm weights), and kv_bytes(pos) is the f32 key and
+    value rows 0..pos read plus row pos written, per layer, counted here
+    element by element from the cache layout [layer][position][kv_dim]."""
+    m = llama.make_model(cfg, seed=0)
+    assert cfg.int8_weight_bytes() == sum(v.nbytes for k, v in m.items() if k != "rope")
+    for pos in (0, 1, cfg.seq_len - 1):
+        rows_read = pos + 1
+        per_layer = 2 * (rows_read + 1) * cfg.kv_dim * np.dtype(np.float32).itemsize
+        assert cfg.kv_bytes(pos) == cfg.n_layers * per_layer
