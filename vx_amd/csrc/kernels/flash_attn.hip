@@ -68,6 +68,12 @@ constexpr int kThreads = 256;
 #ifndef VX_FA_SGB
 #define VX_FA_SGB 3
 #endif
+/* V^T reads issued ahead of the first PV MFMA (0: the compiler's order).
+ * 8 measured 1-2% faster than the compiler's order on config 3 (paired runs;
+ * 4 and 12 within noise of 8). */
+#ifndef VX_FA_PV_LEAD
+#define VX_FA_PV_LEAD 8
+#endif
 constexpr float kSlack = 8.0f; /* base-2 headroom of the stale row max */
 /* Heads an XCD works through together (0: all of its heads at once). */
 #ifndef VX_FA_HG
@@ -421,6 +427,18 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
         }
       }
     }
+#if VX_FA_PV_LEAD > 0
+    /* The transposing reads run VX_FA_PV_LEAD reads (a few MFMAs) ahead of
+     * the MFMAs that consume them, then two per MFMA. */
+    __builtin_amdgcn_sched_group_barrier(0x100, VX_FA_PV_LEAD, 0); /* DS read */
+#pragma unroll
+    for (int g = 0; g < (2 * kKS * kDTiles - VX_FA_PV_LEAD) / 2; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* MFMA */
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(
+        0x008, kKS * kDTiles - (2 * kKS * kDTiles - VX_FA_PV_LEAD) / 2, 0);
+#endif
   };
 
   /* One key block. Entering it, K of this block and the next and V of this
