@@ -327,6 +327,49 @@ def bench_fa(lib, timer, steps: int, warmup: int):
                           "traffic": traffic_from_profiles("fa_causal_4x32x2048x128")})
 
 
+def bench_fa_chunks(lib, timer, steps: int = 20):
+    """The reference's own flash-attention benchmark shape (reference
+    benchmarks/apple_gpu_mlir_kernels/README.md:30-37): a 512-token causal
+    prefill chunk at position 0, 1536 and 7680, 32 query heads over 4 KV
+    heads, head_dim 128, bf16 (the reference's kernel reads f16 K/V on an
+    Apple M4, 1.26 / 7.6 / 33.6 ms: context, not a target). Microseconds per
+    call and TFLOP/s over the causal work."""
+    from vx_amd import abi
+    from vx_amd.abi import f32_to_bf16
+    from vx_amd.runtime import DeviceArray, flash_attention_fwd
+
+    out = {}
+    rng = np.random.default_rng(9)
+    b, h, hk, sq, d = 1, 32, 4, 512, 128
+    for start in (0, 1536, 7680):
+        sk = start + sq
+        q = DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((b, h, sq, d)).astype(np.float32)),
+                           abi.DTYPE_BF16)
+        k = DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((b, hk, sk, d)).astype(np.float32)),
+                           abi.DTYPE_BF16)
+        v = DeviceArray.of(lib, f32_to_bf16(rng.standard_normal((b, hk, sk, d)).astype(np.float32)),
+                           abi.DTYPE_BF16)
+        o = DeviceArray(lib, (b, h, sq, d), abi.DTYPE_BF16)
+        lse = DeviceArray(lib, (b, h, sq), abi.DTYPE_F32)
+
+        def call():
+            assert flash_attention_fwd(lib, q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, b, h, hk, sq, sk,
+                                       d, 1.0 / np.sqrt(d), True) == 0
+
+        for _ in range(3):
+            call()
+        timer.sync()
+        runs = timed_runs(call, timer, steps)
+        us = float(np.median(runs)) * 1e3
+        # query i sees start + i + 1 keys
+        flops = 4.0 * b * h * d * float(np.sum(start + np.arange(sq) + 1))
+        out[str(start)] = dict(us=round(us, 2), tflops=round(flops / (us * 1e-6) / 1e12, 1),
+                               runs_us=spread([x * 1e3 for x in runs]))
+        for x in (q, k, v, o, lse):
+            x.free()
+    return out
+
+
 def bench_gemv(lib, timer, steps: int, warmup: int):
     """BASELINE config 5 through vx_nn_gemv_i8_bf16. Each shape rotates
     through enough weight copies to exceed twice the 256 MB MALL, so every
@@ -477,6 +520,7 @@ def main() -> int:
     if "fa" in only:
         log("flash attention config 3")
         extra["flash_attn_fwd"] = bench_fa(lib, timer, max(10, ns.steps // 2), 3)
+        extra["flash_attn_prefill_chunks"] = bench_fa_chunks(lib, timer)
         log(f"fa {extra['flash_attn_fwd']['tflops']:.1f} TFLOP/s")
     if "gemv" in only:
         log("int8 gemv config 5")

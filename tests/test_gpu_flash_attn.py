@@ -99,6 +99,29 @@ def test_baseline_config_sampled(hiplib):
     assert np.isfinite(o).all()
 
 
+@pytest.mark.parametrize("start", [0, 1536, 7680])
+def test_reference_prefill_chunks(hiplib, start):
+    """The reference's own flash-attention benchmark shape (reference
+    benchmarks/apple_gpu_mlir_kernels/README.md:30-37): a 512-token causal
+    prefill chunk at position 0, 1536 and 7680 of the cache, 32 query heads
+    over 4 KV heads, head_dim 128. Queries sit at the end of the keys
+    (seq_k = start + 512), so query i sees keys up to start + i. Sampled rows
+    against the f64 oracle."""
+    announce(f"flash attn prefill chunk at {start}")
+    rng = np.random.default_rng(start + 5)
+    b, h, hk, sq, d = 1, 32, 4, 512, 128
+    sk = start + sq
+    q16, k16, v16 = randn16(rng, (b, h, sq, d)), randn16(rng, (b, hk, sk, d)), randn16(rng, (b, hk, sk, d))
+    scale = 1.0 / np.sqrt(d)
+    o, lse = run(hiplib, q16, k16, v16, h, hk, scale, True)
+    picks = [0, 1, 63, 64, 255, 256, 510, 511]
+    rows = np.array([(0, hi, qi) for hi in (0, 7, 8, 31) for qi in picks], np.int64)
+    wo, wl = oracle.attention_rows(q16, k16, v16, h, hk, scale, True, rows)
+    assert_max_abs(o[rows[:, 0], rows[:, 1], rows[:, 2]], wo, BF16_ABS, f"chunk at {start}")
+    assert_max_abs(lse[rows[:, 0], rows[:, 1], rows[:, 2]], wl, 1e-3, f"chunk lse at {start}")
+    assert np.isfinite(o).all()
+
+
 def test_no_lse_and_refusals(hiplib, rng):
     announce("flash attn refusals")
     q16 = randn16(rng, (1, 2, 64, 64))
