@@ -356,15 +356,25 @@ def bench_fa_chunks(lib, timer, steps: int = 20):
             assert flash_attention_fwd(lib, q.ptr, k.ptr, v.ptr, o.ptr, lse.ptr, b, h, hk, sq, sk,
                                        d, 1.0 / np.sqrt(d), True) == 0
 
-        for _ in range(3):
-            call()
-        timer.sync()
-        runs = timed_runs(call, timer, steps)
-        us = float(np.median(runs)) * 1e3
         # query i sees start + i + 1 keys
         flops = 4.0 * b * h * d * float(np.sum(start + np.arange(sq) + 1))
-        out[str(start)] = dict(us=round(us, 2), tflops=round(flops / (us * 1e-6) / 1e12, 1),
-                               runs_us=spread([x * 1e3 for x in runs]))
+        row = {}
+        # the library's own choice (these 128 query blocks get a key split),
+        # then the same call forced unsplit
+        for key, splits in (("", 0), ("unsplit_", 1)):
+            lib.force_fa_splits(splits)
+            try:
+                for _ in range(3):
+                    call()
+                timer.sync()
+                runs = timed_runs(call, timer, steps)
+            finally:
+                lib.force_fa_splits(0)
+            us = float(np.median(runs)) * 1e3
+            row[key + "us"] = round(us, 2)
+            row[key + "tflops"] = round(flops / (us * 1e-6) / 1e12, 1)
+            row[key + "runs_us"] = spread([x * 1e3 for x in runs])
+        out[str(start)] = row
         for x in (q, k, v, o, lse):
             x.free()
     return out

@@ -122,6 +122,60 @@ def test_reference_prefill_chunks(hiplib, start):
     assert np.isfinite(o).all()
 
 
+SPLIT_CASES = [
+    # batch, heads, kv_heads, seq_q, seq_k, head_dim, causal, splits
+    (1, 4, 2, 1, 1000, 128, True, 4),      # one query row over a long cache
+    (1, 2, 1, 64, 700, 128, True, 3),      # queries at the end of the keys, GQA
+    (2, 2, 2, 200, 200, 64, True, 4),      # causal square: late splits empty for early rows
+    (1, 3, 3, 129, 577, 64, False, 5),     # ragged key tail, non-causal
+    (1, 2, 2, 300, 70, 128, True, 8),      # more splits than key blocks (clamped)
+    (1, 2, 2, 64, 4100, 128, False, 64),   # the largest forced count
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_key_splits_match_oracle(hiplib, case, rng):
+    """Key-split launches (each split's partial in f32, then the merge) on
+    shapes the automatic choice would not split: every row against the
+    oracle, and the split output against the unsplit launch of the same
+    inputs. Rows no split saw (causal rows with no key) must merge to o = 0
+    and lse = -inf."""
+    announce(f"flash attn split {case}")
+    b, h, hk, sq, sk, d, causal, splits = case
+    q16, k16, v16 = randn16(rng, (b, h, sq, d)), randn16(rng, (b, hk, sk, d)), randn16(rng, (b, hk, sk, d))
+    scale = 1.0 / np.sqrt(d)
+    hiplib.force_fa_splits(splits)
+    try:
+        o, lse = run(hiplib, q16, k16, v16, h, hk, scale, causal)
+        o_nolse, _ = run(hiplib, q16, k16, v16, h, hk, scale, causal, with_lse=False)
+    finally:
+        hiplib.force_fa_splits(0)
+    hiplib.force_fa_splits(1)
+    try:
+        o1, lse1 = run(hiplib, q16, k16, v16, h, hk, scale, causal)
+    finally:
+        hiplib.force_fa_splits(0)
+    rows = oracle.attention_all_rows(b, h, sq)
+    wo, wl = oracle.attention_rows(q16, k16, v16, h, hk, scale, causal, rows)
+    assert_max_abs(o.reshape(-1, d), wo, BF16_ABS, f"split o {case}")
+    fin = np.isfinite(wl)
+    assert np.array_equal(np.isfinite(lse.ravel()), fin)
+    assert_max_abs(lse.ravel()[fin], wl[fin], 1e-3, f"split lse {case}")
+    assert np.all(o.reshape(-1, d)[~fin] == 0)
+    assert np.array_equal(o, o_nolse)
+    # the split and unsplit launches differ only by f32 rounding in the merge
+    assert_max_abs(o.reshape(-1, d), o1.reshape(-1, d), BF16_ABS, f"split vs unsplit {case}")
+    assert_max_abs(lse.ravel()[fin], lse1.ravel()[fin], 1e-4, f"split vs unsplit lse {case}")
+
+
+def test_split_control_refusals(hiplib):
+    with pytest.raises(ValueError):
+        hiplib.force_fa_splits(-1)
+    with pytest.raises(ValueError):
+        hiplib.force_fa_splits(65)
+    hiplib.force_fa_splits(0)
+
+
 def test_no_lse_and_refusals(hiplib, rng):
     announce("flash attn refusals")
     q16 = randn16(rng, (1, 2, 64, 64))

@@ -1282,6 +1282,7 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
 #define VX_HIP_CTRL_IMAGE_STATS (VX_CTRL_VENDOR_BASE + 4)
 #define VX_HIP_CTRL_CLOCK_STAMPS (VX_CTRL_VENDOR_BASE + 5)
 #define VX_HIP_CTRL_GEMV_KERNEL (VX_CTRL_VENDOR_BASE + 6)
+#define VX_HIP_CTRL_FA_SPLITS (VX_CTRL_VENDOR_BASE + 7)
 
 int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   switch (opcode) {
@@ -1401,6 +1402,17 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
       return 0;
     }
     vxk::gemv_i8_force(static_cast<vxk::GemvKernel>(*which));
+    return 1;
+  }
+  case VX_HIP_CTRL_FA_SPLITS: {
+    /* payload -> int32_t: 0 automatic, n in 1..64 cuts every flash-attention
+     * launch's key range into n splits (fewer when there are fewer key
+     * blocks) wherever splitting is allowed. */
+    const int32_t *splits = static_cast<const int32_t *>(payload);
+    if (!splits || *splits < 0 || *splits > 64) {
+      return 0;
+    }
+    vxk::flash_attn_force_splits(*splits);
     return 1;
   }
   case VX_HIP_CTRL_POOL_DRAIN:

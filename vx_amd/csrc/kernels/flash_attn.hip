@@ -31,11 +31,24 @@
  * the next block's score MFMAs are issued while this block's softmax runs.
  * Workgroups start with the heaviest query blocks (causal work grows with
  * the block index); each XCD keeps a few heads' K/V in its L2 at a time.
+ *
+ * Key splits: when the query blocks alone give fewer workgroups than one
+ * round of two per CU (a 512-query prefill chunk over a long cache gives
+ * 128), the key range is cut into splits, each workgroup writes its rows'
+ * normalised output and log-sum-exp in f32, and a second kernel merges
+ * them (the flash-decoding merge). Merging inside the split kernel (the
+ * last workgroup of a block combining) measured slower: the device-scope
+ * release and acquire it needs write back and invalidate the whole L2 of
+ * the XCD, so the other workgroups lose their K/V lines.
  */
 #include "../vx_hip_common.h"
 #include "../vx_ops_kernels.h"
 
+#include <algorithm>
+#include <atomic>
 #include <cmath>
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 namespace vxk {
@@ -48,6 +61,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 #define VX_LDS __attribute__((address_space(3)))
 
@@ -164,12 +178,13 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
 
 /* kQT query tiles of 32 per wave: a wave owns 32 * kQT queries, so each K
  * and V operand read from LDS feeds kQT MFMAs. */
-template <int kD, int kQT, int kBK>
+template <int kD, int kQT, int kBK, bool kSplit>
 __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     const uint16_t *__restrict__ Q, const uint16_t *__restrict__ K,
     const uint16_t *__restrict__ V, uint16_t *__restrict__ O,
     float *__restrict__ LSE, int heads, int group, int seq_q, int seq_k,
-    int bh_total, int q_blocks, float scale_log2, bool causal) {
+    int bh_total, int q_blocks, float scale_log2, bool causal, int splits,
+    float *__restrict__ Opart, float *__restrict__ Lpart) {
   constexpr int kBlockK = kBK;                    /* keys per block */
   constexpr int kKT = kBlockK / 32;               /* 32-key tiles per block */
   constexpr int kKS = kBlockK / 16;               /* 16-key MFMA steps */
@@ -195,6 +210,13 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
    * (all query blocks of the group, heaviest first), which keeps the K/V of
    * only a few heads live in its L2 at once. */
   int id = blockIdx.x;
+  /* Split mode: workgroup (item, sp) takes key blocks sp * per .. of its
+   * item, per = ceil(key blocks of the whole sequence / splits). */
+  int sp = 0;
+  if constexpr (kSplit) {
+    sp = id % splits;
+    id /= splits;
+  }
   int bh, qb;
   if ((bh_total & 7) == 0) {
     const int xcd = id & 7;
@@ -233,7 +255,13 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     kv_end = min(seq_k, q0 + kBlockQ + shift);
     wave_last = min(seq_k - 1, qw0 + kWaveQ - 1 + shift);
   }
-  const int nblocks = kv_end > 0 ? (kv_end + kBlockK - 1) / kBlockK : 0;
+  int nblocks = kv_end > 0 ? (kv_end + kBlockK - 1) / kBlockK : 0;
+  int first = 0; /* first key block of this workgroup */
+  if constexpr (kSplit) {
+    const int per = ((seq_k + kBlockK - 1) / kBlockK + splits - 1) / splits;
+    first = sp * per;
+    nblocks = min(nblocks, first + per);
+  }
 
   /* The wave's Q^T as MFMA B operands: lane (q = lq, group g) of tile qt
    * holds d = 16s + 8g .. +8 of query qw0 + 32 qt + lq for each d-step s. */
@@ -521,19 +549,19 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
   };
 
   Scores sa, sb;
-  if (nblocks > 0) {
-    issue(0, 0);
-    issue(0, 1);
-    if (nblocks > 1) {
-      issue(1, 0);
+  if (first < nblocks) {
+    issue(first, 0);
+    issue(first, 1);
+    if (first + 1 < nblocks) {
+      issue(first + 1, 0);
     }
     wait_all_loads();
     lds_barrier();
-    if (0 <= wave_last) {
-      scores(0, sa);
+    if (first * kBlockK <= wave_last) {
+      scores(first, sa);
     }
   }
-  for (int blk = 0; blk < nblocks; blk += 2) {
+  for (int blk = first; blk < nblocks; blk += 2) {
     step(blk, sa, sb);
     if (blk + 1 < nblocks) {
       step(blk + 1, sb, sa);
@@ -547,6 +575,31 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
       continue;
     }
     const float inv = l_run[qt] > 0.0f ? 1.0f / l_run[qt] : 0.0f;
+    if constexpr (kSplit) {
+      /* This split's normalised output and log-sum-exp, in f32, for the
+       * merge: part sp of [splits][bh_total][seq_q]. A row the split never
+       * saw writes only its lse (-inf); the merge reads no output for it. */
+      const int64_t row = ((int64_t)sp * bh_total + bh) * seq_q + my_q;
+      if (l_run[qt] > 0.0f) {
+        float *prow = Opart + row * kD;
+#pragma unroll
+        for (int i = 0; i < kDTiles; ++i) {
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = i * 32 + 8 * r4 + 4 * g;
+            *reinterpret_cast<f32x4v *>(prow + d) = f32x4v{
+                o_acc[qt][i][4 * r4] * inv, o_acc[qt][i][4 * r4 + 1] * inv,
+                o_acc[qt][i][4 * r4 + 2] * inv, o_acc[qt][i][4 * r4 + 3] * inv};
+          }
+        }
+      }
+      if (g == 0) {
+        Lpart[row] = l_run[qt] > 0.0f
+                         ? (m_run[qt] + log2f(l_run[qt])) * 0.69314718055994531f
+                         : -INFINITY;
+      }
+      continue;
+    }
     uint16_t *orow = O + q_base + (int64_t)my_q * kD;
 #pragma unroll
     for (int i = 0; i < kDTiles; ++i) {
@@ -569,24 +622,168 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
   }
 }
 
+/* Merge of the key splits' partials (the flash-decoding merge, as
+ * reference stdlib/std/nn.vx's attention parts and merge). Per row: M the
+ * largest split lse, w_s = e^(lse_s - M) (0 for a split that saw no key),
+ * o = sum_s w_s o_s / sum_s w_s rounded to bf16 once, lse = M + ln sum_s
+ * w_s; a row no split saw gets o = 0 and lse = -inf. kD / 4 threads per
+ * row, four columns each. Every split's lse is read first and every output
+ * load issued before any is used (an unseen split's output is not written
+ * by the split kernel and is dropped by a select, never multiplied). */
+template <int kD>
+__global__ __launch_bounds__(256) void flash_merge(
+    const float *__restrict__ Opart, const float *__restrict__ Lpart,
+    uint16_t *__restrict__ O, float *__restrict__ LSE, int64_t rows,
+    int splits) {
+  constexpr int kVec = kD / 4;
+  constexpr int kBatch = 4; /* splits combined per round of loads */
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = t / kVec;
+  const int c = (int)(t % kVec);
+  if (row >= rows) {
+    return;
+  }
+  float mx = -INFINITY;
+  for (int s = 0; s < splits; ++s) {
+    mx = fmaxf(mx, Lpart[s * rows + row]);
+  }
+  float sum = 0.0f;
+  f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (mx != -INFINITY) {
+    for (int s0 = 0; s0 < splits; s0 += kBatch) {
+      float l[kBatch];
+      f32x4v ov[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int s = min(s0 + j, splits - 1);
+        l[j] = s0 + j < splits ? Lpart[s * rows + row] : -INFINITY;
+        ov[j] = *reinterpret_cast<const f32x4v *>(Opart + (s * rows + row) * kD +
+                                                  4 * c);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const bool seen = l[j] != -INFINITY;
+        const float w = seen ? expf(l[j] - mx) : 0.0f;
+        sum += w;
+        acc[0] += seen ? w * ov[j][0] : 0.0f;
+        acc[1] += seen ? w * ov[j][1] : 0.0f;
+        acc[2] += seen ? w * ov[j][2] : 0.0f;
+        acc[3] += seen ? w * ov[j][3] : 0.0f;
+      }
+    }
+  }
+  const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+  u32x2 out;
+  out[0] = pack2(acc[0] * inv, acc[1] * inv);
+  out[1] = pack2(acc[2] * inv, acc[3] * inv);
+  *reinterpret_cast<u32x2 *>(O + row * kD + 4 * c) = out;
+  if (LSE && c == 0) {
+    LSE[row] = sum > 0.0f ? mx + logf(sum) : -INFINITY;
+  }
+}
+
 template <int kD, int kQT, int kBK>
 void launch(const uint16_t *q, const uint16_t *k, const uint16_t *v,
             uint16_t *o, float *lse, int heads, int group, int seq_q, int seq_k,
-            int bh, float scale_log2, bool causal, hipStream_t stream) {
+            int bh, float scale_log2, bool causal, int splits, float *opart,
+            float *lpart, hipStream_t stream) {
   constexpr int kBlockQ = 4 * 32 * kQT;
   const int qblocks = (seq_q + kBlockQ - 1) / kBlockQ;
-  hipLaunchKernelGGL((flash_fwd<kD, kQT, kBK>), dim3((unsigned)(bh * qblocks)),
-                     dim3(kThreads), 0, stream, q, k, v, o, lse, heads, group,
-                     seq_q, seq_k, bh, qblocks, scale_log2, causal);
+  if (splits <= 1) {
+    hipLaunchKernelGGL((flash_fwd<kD, kQT, kBK, false>),
+                       dim3((unsigned)(bh * qblocks)), dim3(kThreads), 0, stream,
+                       q, k, v, o, lse, heads, group, seq_q, seq_k, bh, qblocks,
+                       scale_log2, causal, 1, nullptr, nullptr);
+    return;
+  }
+  hipLaunchKernelGGL((flash_fwd<kD, kQT, kBK, true>),
+                     dim3((unsigned)(bh * qblocks * splits)), dim3(kThreads), 0,
+                     stream, q, k, v, o, lse, heads, group, seq_q, seq_k, bh,
+                     qblocks, scale_log2, causal, splits, opart, lpart);
+  const int64_t rows = (int64_t)bh * seq_q;
+  const int64_t threads = rows * (kD / 4);
+  hipLaunchKernelGGL((flash_merge<kD>), dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, stream, opart, lpart, o, lse, rows, splits);
+}
+
+std::atomic<int> forced_splits{0};
+
+/* Key splits for a launch: the query blocks alone give `items` workgroups.
+ * Below one round of two per CU, and with at least 16 key blocks, the key
+ * range is cut so that about one such round runs: at least 8 key blocks per
+ * split, at most 8 splits (measured on the 512-query prefill chunks over
+ * 2048 and 8192 keys: 4 splits of 128 items fastest, 6 and 8 slower; no
+ * split pays over 512 keys). */
+int pick_splits(int64_t items, int64_t key_blocks, int cus) {
+  const int forced = forced_splits.load();
+  if (forced > 0) {
+    return (int)std::min<int64_t>(forced, std::max<int64_t>(key_blocks, 1));
+  }
+  const int64_t slots = 2 * (int64_t)cus;
+  if (items >= slots || key_blocks < 16) {
+    return 1;
+  }
+  const int64_t want = (slots + items - 1) / items;
+  return (int)std::max<int64_t>(1, std::min<int64_t>({want, 8, key_blocks / 8}));
+}
+
+/* Split partials of one (device, stream). Launches on one stream run in
+ * order, so they share the block; it grows (the old block freed in the
+ * stream's order) and lives until the process ends. */
+struct SplitSpace {
+  float *base = nullptr;
+  size_t bytes = 0;
+};
+std::mutex spaces_mutex;
+std::map<std::pair<int, hipStream_t>, SplitSpace> &spaces() {
+  static auto *m = new std::map<std::pair<int, hipStream_t>, SplitSpace>();
+  return *m;
+}
+
+/* Makes `sp` hold `bytes` on `stream` (caller holds spaces_mutex); false
+ * when the memory cannot be had. */
+bool reserve(SplitSpace &sp, size_t bytes, hipStream_t stream) {
+  if (sp.base && bytes <= sp.bytes) {
+    return true;
+  }
+  void *fresh = nullptr;
+  if (hipMallocAsync(&fresh, bytes, stream) != hipSuccess || !fresh) {
+    (void)hipGetLastError();
+    return false;
+  }
+  if (sp.base) {
+    VX_HIP_CHECK(hipFreeAsync(sp.base, stream));
+  }
+  sp.base = static_cast<float *>(fresh);
+  sp.bytes = bytes;
+  return true;
+}
+
+int device_cus() {
+  static std::atomic<int> cached{0};
+  int n = cached.load();
+  if (n == 0) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    n = hipGetDevice(&dev) == hipSuccess &&
+                hipGetDeviceProperties(&prop, dev) == hipSuccess
+            ? prop.multiProcessorCount
+            : 256;
+    cached.store(n);
+  }
+  return n;
 }
 
 } // namespace
+
+void flash_attn_force_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0); }
 
 bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
                            const uint16_t *v, uint16_t *o, float *lse,
                            int64_t batch, int64_t heads, int64_t kv_heads,
                            int64_t seq_q, int64_t seq_k, int64_t head_dim,
-                           float scale, bool causal, hipStream_t stream) {
+                           float scale, bool causal, bool allow_split,
+                           hipStream_t stream) {
   for (const void *p : {(const void *)q, (const void *)k, (const void *)v,
                         (const void *)o}) {
     if (reinterpret_cast<uintptr_t>(p) & 15) {
@@ -605,12 +802,51 @@ bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
   }
   const float scale_log2 = scale * 1.4426950408889634f;
   const int group = (int)(heads / kv_heads);
+  constexpr int kBlockQ = 4 * 32 * VX_FA_QT;
+  const int64_t items = bh * ((seq_q + kBlockQ - 1) / kBlockQ);
+  const int64_t key_blocks = (seq_k + VX_FA_BK - 1) / VX_FA_BK;
+  int splits = allow_split ? pick_splits(items, key_blocks, device_cus()) : 1;
+  /* Both grids stay within 32-bit workgroup and thread counts. */
+  if (items * splits > INT32_MAX || bh * seq_q * (head_dim / 4) > INT32_MAX) {
+    splits = 1;
+  }
+  if (splits > 1) {
+    /* Held from the workspace lookup through the launch, so a growth on one
+     * thread cannot free a block another thread's launch is about to use. */
+    std::lock_guard<std::mutex> hold(spaces_mutex);
+    int dev = 0;
+    VX_HIP_CHECK(hipGetDevice(&dev));
+    SplitSpace &sp = spaces()[{dev, stream}];
+    const size_t rows = (size_t)bh * (size_t)seq_q;
+    const size_t bytes =
+        (size_t)splits * rows * ((size_t)head_dim + 1) * sizeof(float);
+    if (reserve(sp, bytes, stream)) {
+      float *opart = sp.base;
+      float *lpart = opart + (size_t)splits * rows * (size_t)head_dim;
+      if (head_dim == 128) {
+        launch<128, VX_FA_QT, VX_FA_BK>(q, k, v, o, lse, (int)heads, group,
+                                        (int)seq_q, (int)seq_k, (int)bh,
+                                        scale_log2, causal, splits, opart, lpart,
+                                        stream);
+      } else {
+        launch<64, VX_FA_QT, VX_FA_BK>(q, k, v, o, lse, (int)heads, group,
+                                       (int)seq_q, (int)seq_k, (int)bh,
+                                       scale_log2, causal, splits, opart, lpart,
+                                       stream);
+      }
+      VX_HIP_CHECK(hipGetLastError());
+      return true;
+    }
+    splits = 1; /* no workspace: run unsplit */
+  }
   if (head_dim == 128) {
     launch<128, VX_FA_QT, VX_FA_BK>(q, k, v, o, lse, (int)heads, group, (int)seq_q,
-                          (int)seq_k, (int)bh, scale_log2, causal, stream);
+                          (int)seq_k, (int)bh, scale_log2, causal, 1, nullptr,
+                          nullptr, stream);
   } else {
     launch<64, VX_FA_QT, VX_FA_BK>(q, k, v, o, lse, (int)heads, group, (int)seq_q,
-                         (int)seq_k, (int)bh, scale_log2, causal, stream);
+                         (int)seq_k, (int)bh, scale_log2, causal, 1, nullptr,
+                         nullptr, stream);
   }
   VX_HIP_CHECK(hipGetLastError());
   return true;

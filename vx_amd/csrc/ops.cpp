@@ -94,9 +94,11 @@ int32_t vx_nn_flash_attention_fwd_bf16(const uint16_t *q, const uint16_t *k,
   if (!all_on_device({q, k, v, o, lse})) {
     return refuse(VX_OP_ENOTDEV, op, "every operand must be GPU memory");
   }
+  /* Splitting takes HBM for the partials in the stream's order; a graph
+   * being captured gets the unsplit launch. */
   if (!vxk::flash_attn_fwd_launch(q, k, v, o, lse, batch, heads, kv_heads,
                                   seq_q, seq_k, head_dim, scale, causal != 0,
-                                  vxops::stream())) {
+                                  !vxops::capturing(), vxops::stream())) {
     return refuse(VX_OP_EUNSUPP, op, "operands must be 16-byte aligned");
   }
   vxops::launched(op);

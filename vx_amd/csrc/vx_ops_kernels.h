@@ -35,12 +35,19 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
                     hipStream_t stream);
 
 /* Flash-attention forward; layout as include/vx_hip_ops.h. head_dim 64 or
- * 128, seq lengths >= 1. */
+ * 128, seq lengths >= 1. With `allow_split`, a launch whose query blocks
+ * fill less than one round of the GPU cuts the key range into splits (their
+ * partials in HBM taken in the stream's order) and merges them. */
 bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
                            const uint16_t *v, uint16_t *o, float *lse,
                            int64_t batch, int64_t heads, int64_t kv_heads,
                            int64_t seq_q, int64_t seq_k, int64_t head_dim,
-                           float scale, bool causal, hipStream_t stream);
+                           float scale, bool causal, bool allow_split,
+                           hipStream_t stream);
+
+/* Force the key splits of flash_attn_fwd_launch (0: the automatic choice;
+ * a forced count applies where splitting is allowed). */
+void flash_attn_force_splits(int splits);
 
 } // namespace vxk
 

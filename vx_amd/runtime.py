@@ -136,6 +136,13 @@ class DispatchLibrary:
         if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMV_KERNEL, ctypes.byref(v)):
             raise ValueError(f"no GEMV kernel {which}")
 
+    def force_fa_splits(self, splits: int) -> None:
+        """Cut every flash-attention launch's key range into `splits` parts
+        (0: the automatic choice; graph capture always runs unsplit)."""
+        v = ctypes.c_int32(splits)
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_FA_SPLITS, ctypes.byref(v)):
+            raise ValueError(f"no flash-attention split count {splits}")
+
     def clock_stamps(self, base: int | None, slots: int) -> None:
         """Have routed MFMA GEMMs record their clock counters (4 x u64 per
         launch: shader clock and 100 MHz real-time counter at the start and
