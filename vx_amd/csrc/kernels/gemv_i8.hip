@@ -468,11 +468,23 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
   }
 }
 
+/* Waves per workgroup and tile width of the 16-row kernel (kR = 1). Sweep
+ * on the config-5 shapes at batches 4, 8 and 16: 4, 8 and 16 waves with
+ * 128-, 256- and 512-column tiles all within 5% of each other. */
+#ifndef VX_GEMV_LDS_W
+#define VX_GEMV_LDS_W 8
+#endif
+#ifndef VX_GEMV_LDS_COLS
+#define VX_GEMV_LDS_COLS 256
+#endif
+
 template <int kR>
 void launch_lds(const int8_t *w, const float *s, const uint16_t *x, float *y,
                 int rows, int cols, int nb, hipStream_t stream) {
   const int grid = (rows + 16 * kR - 1) / (16 * kR);
-  hipLaunchKernelGGL((gemv_i8_lds<8, 256, kR>), dim3(grid), dim3(8 * 64), 0,
+  constexpr int kW = kR == 1 ? VX_GEMV_LDS_W : 8;
+  constexpr int kCols = kR == 1 ? VX_GEMV_LDS_COLS : 256;
+  hipLaunchKernelGGL((gemv_i8_lds<kW, kCols, kR>), dim3(grid), dim3(kW * 64), 0,
                      stream, w, s, x, y, rows, cols, nb);
 }
 
