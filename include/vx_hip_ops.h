@@ -47,7 +47,16 @@ enum {
  * o = softmax(scale * q k^T) v with f32 accumulation, o rounded to bf16 once;
  * lse = natural-log sum of exp of the scaled scores of each row. With
  * `causal`, query i sees key j iff j <= i + (seq_k - seq_q) (the queries are
- * the last seq_q positions). head_dim must be 64 or 128. */
+ * the last seq_q positions). head_dim must be 64 or 128.
+ *
+ * A launch whose query blocks fill less than one round of the GPU (for
+ * example 512 queries of 32 heads over a long cache) may cut the key range
+ * into splits and merge them in f32 (same result to within f32 rounding
+ * before the one bf16 rounding). The split partials live in HBM the
+ * library keeps per (device, stream) for the rest of the process: at most
+ * 8 x batch x heads x seq_q x (head_dim + 1) x 4 bytes, taken in the
+ * stream's order. A stream that is capturing a graph gets the unsplit
+ * launch. */
 int32_t vx_nn_flash_attention_fwd_bf16(const uint16_t *q, const uint16_t *k,
                                        const uint16_t *v, uint16_t *o,
                                        float *lse, int64_t batch, int64_t heads,
