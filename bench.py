@@ -111,16 +111,21 @@ def settle(call, timer, min_ms: float = SETTLE_MS) -> float:
     return spent
 
 
-def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
+def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None = None,
+               k: int | None = None):
+    """C[m, n] = A[m, k] B[k, n] (m = k = n unless given), bf16 in, f32
+    out, through vx_plugin_dispatch_async."""
     from vx_amd import abi
     from vx_amd.abi import f32_to_bf16
     from vx_amd.runtime import DeviceArray, matmul
 
+    m = n if m is None else m
+    k = n if k is None else k
     rng = np.random.default_rng(2024)
-    a16 = f32_to_bf16(rng.normal(0, 1 / 64, (n, n)).astype(np.float32))
-    b16 = f32_to_bf16(rng.normal(0, 1 / 64, (n, n)).astype(np.float32))
+    a16 = f32_to_bf16(rng.normal(0, 1 / 64, (m, k)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1 / 64, (k, n)).astype(np.float32))
     da, db = DeviceArray.of(lib, a16, abi.DTYPE_BF16), DeviceArray.of(lib, b16, abi.DTYPE_BF16)
-    dc = DeviceArray(lib, (n, n), abi.DTYPE_F32)
+    dc = DeviceArray(lib, (m, n), abi.DTYPE_F32)
     ad, bd, cd = da.descriptor(), db.descriptor(), dc.descriptor()
     args = abi.CallArgs()
     args.memref(ad, abi.DTYPE_BF16).scalar(0, abi.KIND_I64).memref(bd, abi.DTYPE_BF16)
@@ -179,9 +184,9 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096):
     assert np.isfinite(c).all()
     for x in (da, db, dc):
         x.free()
-    flops = 2.0 * n * n * n
+    flops = 2.0 * m * n * k
     ms_step = ms_events / steps
-    return dict(n=n, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / steps,
+    return dict(n=n, m=m, k=k, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / steps,
                 tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16,
                 steps_us=spread([x * 1e3 for x in step_ms]), clock_mhz=clock_mhz)
 
@@ -556,6 +561,16 @@ def main() -> int:
                                        tflops=g8["tflops"], frac_of_peak=g8["tflops"] / PEAK_BF16_TFLOPS,
                                        steps_us=g8["steps_us"], clock_mhz=g8["clock_mhz"])
         log(f"gemm 8192 {g8['tflops']:.1f} TFLOP/s")
+        # the reference's own GEMM benchmark shape (benchmarks/gpu_gemm/run.sh:
+        # 8192 x 3072 x 768 beside 4096^3; cuBLAS on an A100 214.2 TFLOP/s,
+        # context only)
+        log("gemm bf16->f32 8192x3072x768 (reference benchmark shape)")
+        gr = bench_gemm(lib, timer, 50, 5, n=3072, m=8192, k=768)
+        extra["gemm_bf16_8192x3072x768"] = dict(
+            config="bf16 x bf16 -> f32 GEMM, M=8192 N=3072 K=768", ms=gr["ms_per_step"],
+            tflops=gr["tflops"], frac_of_peak=gr["tflops"] / PEAK_BF16_TFLOPS,
+            steps_us=gr["steps_us"], clock_mhz=gr["clock_mhz"])
+        log(f"gemm 8192x3072x768 {gr['tflops']:.1f} TFLOP/s")
         log("gemm f32 512^3 (config 1)")
         extra["gemm_f32_512"] = bench_gemm_f32(lib, timer)
         log(f"gemm f32 512: {extra['gemm_f32_512']['us']:.1f} us device, "

@@ -172,13 +172,14 @@ def test_bf16_8192_random(hiplib):
     assert abs(float(c.astype(np.float64).sum()) - sum_invariant(af, bf)) < 5e-2
 
 
-@pytest.mark.parametrize("n", [4096, 8192])
-def test_bf16_small_integers_bit_exact(hiplib, n):
-    """benchmarks/gpu_gemm inputs: every sum exact in f32, so every entry is
-    compared bit for bit (the reference checks 64 samples,
-    v8_tile_128x128_8_subgroups.vx:65-103)."""
-    announce(f"gemm bf16 small ints {n}")
-    a16, b16 = small_int_case(n, n, n)
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 4096), (8192, 8192, 8192), (8192, 3072, 768)])
+def test_bf16_small_integers_bit_exact(hiplib, m, n, k):
+    """benchmarks/gpu_gemm inputs at the reference benchmark's sizes
+    (run.sh: 8192 x 3072 x 768 and 4096^3) and 8192^3: every sum exact in
+    f32, so every entry is compared bit for bit (the reference checks 64
+    samples, v8_tile_128x128_8_subgroups.vx:65-103)."""
+    announce(f"gemm bf16 small ints {m}x{n}x{k}")
+    a16, b16 = small_int_case(m, k, n)
     c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, abi.DTYPE_F32)
     assert st["gemm_mfma"] == 1
     # A's rows repeat with period 7 and B's columns with period 5, so C is a
@@ -186,10 +187,32 @@ def test_bf16_small_integers_bit_exact(hiplib, n):
     a = bf16_to_f32(a16[:7]).astype(np.int64)
     b = bf16_to_f32(b16[:, :5]).astype(np.int64)
     table = (a @ b).astype(np.float32)
-    assert np.array_equal(c, table[np.arange(n)[:, None] % 7, np.arange(n)[None, :] % 5])
+    assert np.array_equal(c, table[np.arange(m)[:, None] % 7, np.arange(n)[None, :] % 5])
     for s in range(64):
-        i, j = (s * 7919) % n, (s * 104729) % n
+        i, j = (s * 7919) % m, (s * 104729) % n
         assert c[i, j] == oracle.gemm_bf16_point_f64(a16, b16, i, j)
+
+
+def test_bf16_reference_benchmark_shape_random(hiplib):
+    """8192 x 3072 x 768 (reference benchmarks/gpu_gemm/run.sh) on N(0, 1/64)
+    operands: sampled rows against the oracle (the reference's loop order)
+    and f64, and the sum invariant."""
+    announce("gemm bf16 8192x3072x768 random")
+    rng = np.random.default_rng(31)
+    m, n, k = 8192, 3072, 768
+    a16 = f32_to_bf16(rng.normal(0, 1 / 64, (m, k)).astype(np.float32))
+    b16 = f32_to_bf16(rng.normal(0, 1 / 64, (k, n)).astype(np.float32))
+    c, st = gpu_gemm(hiplib, a16, b16, abi.DTYPE_BF16, abi.DTYPE_F32)
+    assert st["gemm_mfma"] == 1
+    rows = [0, 1, 255, 256, 4095, 4096, 8190, 8191]
+    af, bf = bf16_to_f32(a16), bf16_to_f32(b16)
+    want = oracle.gemm_bf16_f32(a16[rows], b16)
+    exact = af[rows].astype(np.float64) @ bf.astype(np.float64)
+    for i, r in enumerate(rows):
+        assert_max_abs(c[r], want[i], 1e-4, f"row {r} vs oracle")
+        assert_max_abs(c[r], exact[i], 1e-4, f"row {r} vs f64")
+    assert np.isfinite(c).all()
+    assert abs(float(c.astype(np.float64).sum()) - sum_invariant(af, bf)) < 5e-2
 
 
 def test_bf16_out_and_f16(hiplib, rng):
