@@ -9,7 +9,7 @@ from tests.conftest import announce
 from tests.parity import BF16_ABS, assert_max_abs
 from vx_amd import abi
 from vx_amd.abi import bf16_to_f32, f32_to_bf16
-from vx_amd.runtime import DeviceArray, flash_attention_fwd
+from vx_amd.runtime import DeviceArray, HipTimer, flash_attention_fwd
 
 pytestmark = pytest.mark.gpu
 
@@ -166,6 +166,57 @@ def test_key_splits_match_oracle(hiplib, case, rng):
     # the split and unsplit launches differ only by f32 rounding in the merge
     assert_max_abs(o.reshape(-1, d), o1.reshape(-1, d), BF16_ABS, f"split vs unsplit {case}")
     assert_max_abs(lse.ravel()[fin], lse1.ravel()[fin], 1e-4, f"split vs unsplit lse {case}")
+
+
+def test_capture_runs_unsplit(hiplib, rng):
+    """A launch recorded into a hipGraph takes no stream-ordered workspace,
+    so it runs unsplit even with splits forced: every replay (with eager
+    launches that overwrite O in between) equals the eager unsplit launch
+    bit for bit, and the eager split launch matches it to rounding."""
+    announce("flash attn captured with splits forced")
+    b, h, hk, sq, sk, d = 1, 32, 4, 512, 2048, 128
+    q16, k16, v16 = randn16(rng, (b, h, sq, d)), randn16(rng, (b, hk, sk, d)), randn16(rng, (b, hk, sk, d))
+    q2 = randn16(rng, (b, h, sq, d))
+    scale = 1.0 / np.sqrt(d)
+    dq, dq2 = DeviceArray.of(hiplib, q16, abi.DTYPE_BF16), DeviceArray.of(hiplib, q2, abi.DTYPE_BF16)
+    dk, dv = DeviceArray.of(hiplib, k16, abi.DTYPE_BF16), DeviceArray.of(hiplib, v16, abi.DTYPE_BF16)
+    do = DeviceArray(hiplib, (b, h, sq, d), abi.DTYPE_BF16)
+    dl = DeviceArray(hiplib, (b, h, sq), abi.DTYPE_F32)
+
+    def call(qp):
+        assert flash_attention_fwd(hiplib, qp, dk.ptr, dv.ptr, do.ptr, dl.ptr, b, h, hk, sq, sk, d,
+                                   scale, True) == 0
+
+    t = HipTimer()
+    s = t.stream_create()
+    ex = None
+    try:
+        hiplib.force_fa_splits(1)
+        call(dq.ptr)
+        o1, l1 = do.numpy().copy(), dl.numpy().copy()
+        hiplib.force_fa_splits(4)
+        call(dq.ptr)
+        o4, l4 = do.numpy().copy(), dl.numpy().copy()
+        assert_max_abs(bf16_to_f32(o4), bf16_to_f32(o1), BF16_ABS, "split vs unsplit")
+        assert_max_abs(l4, l1, 1e-4, "split vs unsplit lse")
+        hiplib.lib.vx_hip_set_stream(s)
+        ex = t.capture(s, lambda: call(dq.ptr))
+        hiplib.lib.vx_hip_set_stream(None)
+        for rep in range(3):
+            call(dq2.ptr)  # eager, split: overwrites O and LSE
+            hiplib.wait()
+            t.graph_launch(ex, s)
+            t.sync()
+            assert np.array_equal(do.numpy(), o1), f"replay {rep}"
+            assert np.array_equal(dl.numpy(), l1), f"replay {rep} lse"
+    finally:
+        hiplib.force_fa_splits(0)
+        hiplib.lib.vx_hip_set_stream(None)
+        if ex is not None:
+            t.graph_destroy(ex)
+        t.stream_destroy(s)
+        for x in (dq, dq2, dk, dv, do, dl):
+            x.free()
 
 
 def test_split_control_refusals(hiplib):
