@@ -219,6 +219,71 @@ def test_capture_runs_unsplit(hiplib, rng):
             x.free()
 
 
+def test_split_workspaces_from_threads(hiplib):
+    """Four host threads, each on its own stream (the caller stream is per
+    thread), launch the automatically split prefill-chunk shape at two
+    cache lengths in turn, so each stream's partials block grows while the
+    others are in use. The split path is deterministic, so every result must
+    equal the one the same call gives alone."""
+    import threading
+
+    announce("flash attn split workspaces from four threads")
+    b, h, hk, sq, d = 1, 32, 4, 512, 128
+    scale = 1.0 / np.sqrt(d)
+    rng = np.random.default_rng(77)
+    cases = []
+    for sk in (2048, 8192):
+        q16, k16, v16 = (randn16(rng, (b, h, sq, d)), randn16(rng, (b, hk, sk, d)),
+                         randn16(rng, (b, hk, sk, d)))
+        o, lse = run(hiplib, q16, k16, v16, h, hk, scale, True)
+        cases.append((q16, k16, v16, sk, f32_to_bf16(o), lse))
+    errors = []
+
+    def work(tid):
+        t = HipTimer()
+        s = t.stream_create()
+        arrays = []
+        try:
+            hiplib.lib.vx_hip_set_stream(s)
+            dev = []
+            for q16, k16, v16, sk, _, _ in cases:
+                xs = (DeviceArray.of(hiplib, q16, abi.DTYPE_BF16), DeviceArray.of(hiplib, k16, abi.DTYPE_BF16),
+                      DeviceArray.of(hiplib, v16, abi.DTYPE_BF16),
+                      DeviceArray(hiplib, (b, h, sq, d), abi.DTYPE_BF16),
+                      DeviceArray(hiplib, (b, h, sq), abi.DTYPE_F32))
+                arrays += list(xs)
+                dev.append(xs)
+            for it in range(6):
+                ci = (tid + it) % 2
+                dq, dk, dv, do, dl = dev[ci]
+                sk = cases[ci][3]
+                rc = flash_attention_fwd(hiplib, dq.ptr, dk.ptr, dv.ptr, do.ptr, dl.ptr, b, h, hk, sq,
+                                         sk, d, scale, True)
+                if rc != 0:
+                    errors.append((tid, it, f"rc {rc}"))
+                    continue
+                if not np.array_equal(do.numpy(), cases[ci][4]):
+                    errors.append((tid, it, "o"))
+                if not np.array_equal(dl.numpy(), cases[ci][5]):
+                    errors.append((tid, it, "lse"))
+        except Exception as e:  # reported below, with the thread that raised it
+            errors.append((tid, -1, repr(e)))
+        finally:
+            for x in arrays:
+                x.free()
+            hiplib.lib.vx_hip_set_stream(None)
+            t.sync()
+            t.stream_destroy(s)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=90)
+    assert not any(th.is_alive() for th in threads), "a launching thread did not finish"
+    assert not errors, errors
+
+
 def test_split_control_refusals(hiplib):
     with pytest.raises(ValueError):
         hiplib.force_fa_splits(-1)
