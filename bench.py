@@ -480,6 +480,43 @@ def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
                        f"{dt:.1f} s), oracle/vx_oracle.c loop nest, 1 thread")
 
 
+def copy_ceiling(lib, timer, sizes) -> dict:
+    """A measured streaming ceiling beside the 8 TB/s nameplate: the HIP
+    runtime's device-to-device copy (read n bytes, write n bytes) of each
+    size, rotating through enough buffer pairs (over 1 GiB) that every copy
+    streams from and to HBM rather than the 256 MB MALL; 12 copies per timed
+    region, three regions. GB/s counts the bytes read plus written.
+    `sizes` maps a name to a byte count."""
+    import ctypes
+
+    hip = timer.hip
+    hip.hipMemcpyDtoDAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_void_p]
+    out = {}
+    for name, nbytes in sizes.items():
+        pairs = max(4, -(-2**30 // (2 * nbytes)))
+        bufs = [(lib.transfer(None, nbytes), lib.transfer(None, nbytes)) for _ in range(pairs)]
+        turn = [0]
+
+        def call():
+            src, dst = bufs[turn[0] % pairs]
+            turn[0] += 1
+            rc = hip.hipMemcpyDtoDAsync(dst, src, nbytes, None)
+            assert rc == 0, f"hipMemcpyDtoDAsync failed with {rc}"
+
+        for _ in range(pairs):
+            call()
+        timer.sync()
+        runs = timed_runs(call, timer, 12)
+        us = float(np.median(runs)) * 1e3
+        out[name] = dict(bytes=nbytes, us=round(us, 3), gbs=round(2 * nbytes / (us * 1e-6) / 1e9, 1),
+                         runs_us=spread([x * 1e3 for x in runs]), rotated_pairs=pairs)
+        for src, dst in bufs:
+            lib.free(src)
+            lib.free(dst)
+    return out
+
+
 def copy_probe() -> int:
     """A plain copy of known size: 256 MiB read and 256 MiB written per
     launch, three launches."""
@@ -540,6 +577,16 @@ def main() -> int:
     if "gemv" in only:
         log("int8 gemv config 5")
         extra["gemv_i8"] = bench_gemv(lib, timer, max(20, ns.steps), 3)
+        # the weight bytes of each shape copied device to device: what one
+        # dispatch streaming that many bytes reaches on this box
+        ceil = copy_ceiling(lib, timer, {"4096x4096": 4096 * 4096, "11008x4096": 11008 * 4096,
+                                         "256MiB": 256 * 2**20})
+        extra["hbm_copy_ceiling"] = ceil
+        for r in extra["gemv_i8"]:
+            # 11008x4096 and 4096x11008 stream the same 45.1 MB of weights
+            c = ceil["4096x4096" if r["shape"] == [4096, 4096] else "11008x4096"]
+            r["roofline"]["copy_ceiling_gbs"] = c["gbs"]
+            r["roofline"]["frac_of_copy_ceiling"] = round(r["gbs"] / c["gbs"], 4)
         log("gemv " + ", ".join(f"{r['shape'][0]}x{r['shape'][1]}b{r['batch']}:{r['gbs']:.0f}GB/s"
                                 for r in extra["gemv_i8"]))
     if "decode" in only:
