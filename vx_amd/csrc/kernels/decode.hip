@@ -896,10 +896,37 @@ __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) 
 
 constexpr int kChooseThreads = 1024;
 
+/* The better of a and its partner lane's Best (kO = 1, 2, 4, 8: within a
+ * 16-lane row by DPP; 16, 32: across rows by v_permlane16/32_swap, which
+ * hands each lane both halves' values, so merging the two gives the pair's
+ * result in either order). */
+template <int kO> __device__ __forceinline__ Best best_xchg(Best b) {
+  if constexpr (kO <= 8) {
+    Best o;
+    o.v1 = partner<kO>(b.v1);
+    o.i1 = __float_as_int(partner<kO>(__int_as_float(b.i1)));
+    o.v2 = partner<kO>(b.v2);
+    return merge(b, o);
+  } else {
+    auto sw = [](uint32_t x) {
+      return kO == 16 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                      : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    };
+    const auto v1 = sw(__float_as_uint(b.v1));
+    const auto i1 = sw((uint32_t)b.i1);
+    const auto v2 = sw(__float_as_uint(b.v2));
+    return merge(Best{__uint_as_float(v1[0]), (int)i1[0], __uint_as_float(v2[0])},
+                 Best{__uint_as_float(v1[1]), (int)i1[1], __uint_as_float(v2[1])});
+  }
+}
+
 /* Merge the classifier workgroups' partials: argmax with the lowest index
  * winning a tie (reference examples/llama.vx:160-171), or the next prompt
  * token while the prompt lasts; then x = the embedding of that token and
- * pos + 1. */
+ * pos + 1. The candidates and the position are requested first (they
+ * depend on nothing), what the position selects (the prompt token, the
+ * next step's rotary row) as soon as it arrives, so those round trips
+ * overlap the reduction; only the embedding row waits for the choice. */
 __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
                                                               const Best *part,
                                                               int nparts) {
@@ -907,26 +934,26 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
   __shared__ int chosen;
   const int t = threadIdx.x;
   const int lane = t & 63;
+  /* this thread's first candidate in a register (a merge here would wait
+   * for it before the position is requested) */
+  Best b = t < nparts ? part[t] : Best{-INFINITY, 0x7fffffff, -INFINITY};
   const int pos = *a.pos;
   /* The next step's row of the rotary table (pairs for every head offset);
    * none past the cache, where no step follows. */
-  if (pos + 1 < a.seq_len) {
-    for (int i = t; i < a.hs; i += kChooseThreads) {
-      a.rope_now[i] = a.rope[(int64_t)(pos + 1) * a.hs + i];
-    }
-  }
-  Best b{-INFINITY, 0x7fffffff, -INFINITY};
-  for (int i = t; i < nparts; i += kChooseThreads) {
+  const bool next_row = pos + 1 < a.seq_len;
+  const float rope0 =
+      next_row && t < a.hs ? a.rope[(int64_t)(pos + 1) * a.hs + t] : 0.0f;
+  const int prompt_tok =
+      t == 0 && pos + 1 < a.n_prompt ? a.prompt[pos + 1] : 0;
+  for (int i = t + kChooseThreads; i < nparts; i += kChooseThreads) {
     b = merge(b, part[i]);
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    Best o;
-    o.v1 = __shfl_xor(b.v1, off, 64);
-    o.i1 = __shfl_xor(b.i1, off, 64);
-    o.v2 = __shfl_xor(b.v2, off, 64);
-    b = merge(b, o);
-  }
+  b = best_xchg<1>(b);
+  b = best_xchg<2>(b);
+  b = best_xchg<4>(b);
+  b = best_xchg<8>(b);
+  b = best_xchg<16>(b);
+  b = best_xchg<32>(b);
   if (lane == 0) {
     merged[t >> 6] = b;
   }
@@ -938,7 +965,7 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
     }
     int tok;
     if (pos + 1 < a.n_prompt) {
-      tok = a.prompt[pos + 1];
+      tok = prompt_tok;
     } else {
       tok = r.i1;
       const int at = pos + 1 - a.n_prompt;
@@ -956,6 +983,14 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
   const float s = a.tok_s[tok];
   for (int i = t; i < a.dim; i += kChooseThreads) {
     a.x[i] = (float)a.tok_q[(int64_t)tok * a.dim + i] * s;
+  }
+  if (next_row) {
+    if (t < a.hs) {
+      a.rope_now[t] = rope0;
+    }
+    for (int i = t + kChooseThreads; i < a.hs; i += kChooseThreads) {
+      a.rope_now[i] = a.rope[(int64_t)(pos + 1) * a.hs + i];
+    }
   }
   if (t == 0) {
     *a.pos = pos + 1;
