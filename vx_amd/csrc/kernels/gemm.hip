@@ -551,9 +551,12 @@ __global__ __launch_bounds__(256) void gemm_tiled(const void *__restrict__ A,
 #pragma clang fp contract(off)
   using Acc = decltype(load_in<kIn>(nullptr, 0));
   constexpr int kR = kT / 16;        /* outputs per thread per dimension */
-  constexpr int kLoads = kT * 16 / 256;
-  __shared__ Acc As[16][kT + 1]; /* [k][m] */
-  __shared__ Acc Bs[16][kT + 1]; /* [k][n] */
+  /* k per step: deep enough that a step's arithmetic covers the next
+   * step's loads (64 for f32, 32 for f64 to keep the tiles in 33 KiB) */
+  constexpr int kKs = sizeof(Acc) == 8 ? 32 : 64;
+  constexpr int kLoads = kT * kKs / 256;
+  __shared__ Acc As[kKs][kT + 1]; /* [k][m] */
+  __shared__ Acc Bs[kKs][kT + 1]; /* [k][n] */
   const int t = threadIdx.x;
   const int tx = t & 15;
   const int ty = t >> 4;
@@ -567,33 +570,58 @@ __global__ __launch_bounds__(256) void gemm_tiled(const void *__restrict__ A,
       acc[i][j] = Acc(0);
     }
   }
-  for (int64_t k0 = 0; k0 < K; k0 += 16) {
+  /* One kKs-deep step of A and B in registers: the next step's loads are in
+   * flight while this step computes from LDS. */
+  Acc ra[kLoads], rb[kLoads];
+  auto fetch = [&](int64_t k0) {
 #pragma unroll
     for (int e = 0; e < kLoads; ++e) {
       const int idx = t + e * 256;
-      const int am = idx >> 4, ak = idx & 15;
+      const int am = idx / kKs, ak = idx % kKs;
       const int64_t gm = m0 + am, gk = k0 + ak;
-      As[ak][am] = (gm < M && gk < K) ? load_in<kIn>(A, gm * lda + gk) : Acc(0);
+      ra[e] = (gm < M && gk < K) ? load_in<kIn>(A, gm * lda + gk) : Acc(0);
       const int bk = idx / kT, bn = idx % kT;
       const int64_t hk = k0 + bk, hn = n0 + bn;
-      Bs[bk][bn] = (hk < K && hn < N) ? load_in<kIn>(B, hk * ldb + hn) : Acc(0);
+      rb[e] = (hk < K && hn < N) ? load_in<kIn>(B, hk * ldb + hn) : Acc(0);
+    }
+  };
+  auto term = [&](int kk) {
+    Acc a[kR], b[kR];
+#pragma unroll
+    for (int i = 0; i < kR; ++i) {
+      a[i] = As[kk][ty * kR + i];
+      b[i] = Bs[kk][tx * kR + i];
+    }
+#pragma unroll
+    for (int i = 0; i < kR; ++i) {
+#pragma unroll
+      for (int j = 0; j < kR; ++j) {
+        Acc prod = a[i] * b[j];
+        acc[i][j] = acc[i][j] + prod;
+      }
+    }
+  };
+  fetch(0);
+  for (int64_t k0 = 0; k0 < K; k0 += kKs) {
+#pragma unroll
+    for (int e = 0; e < kLoads; ++e) {
+      const int idx = t + e * 256;
+      As[idx % kKs][idx / kKs] = ra[e];
+      Bs[idx / kT][idx % kT] = rb[e];
     }
     __syncthreads();
-    const int kk_end = (K - k0) < 16 ? (int)(K - k0) : 16;
-    for (int kk = 0; kk < kk_end; ++kk) {
-      Acc a[kR], b[kR];
+    if (k0 + kKs < K) {
+      fetch(k0 + kKs);
+    }
+    /* k in order for every output, as before; a full step unrolled */
+    if (K - k0 >= kKs) {
 #pragma unroll
-      for (int i = 0; i < kR; ++i) {
-        a[i] = As[kk][ty * kR + i];
-        b[i] = Bs[kk][tx * kR + i];
+      for (int kk = 0; kk < kKs; ++kk) {
+        term(kk);
       }
-#pragma unroll
-      for (int i = 0; i < kR; ++i) {
-#pragma unroll
-        for (int j = 0; j < kR; ++j) {
-          Acc prod = a[i] * b[j];
-          acc[i][j] = acc[i][j] + prod;
-        }
+    } else {
+      for (int kk = 0; kk < (int)(K - k0); ++kk) {
+        term(kk);
       }
     }
     __syncthreads();
