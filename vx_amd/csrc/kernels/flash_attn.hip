@@ -292,7 +292,9 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
   }
   const uint32_t ring_base =
       (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
-  /* Block b of K and of V lives in slot b % 2 of its plane. */
+  /* Block b of K and of V lives in slot (b - first) % 2 of its plane
+   * (counted from the workgroup's first block, so the loop below, which
+   * steps two blocks at a time from there, sees constant slots). */
   auto issue = [&](int blk, int plane) {
     const int key0 = blk * kBlockK;
     const int bytes = min(kBlockK, seq_k - key0) * kRowBytes;
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     const i32x4 rs = buffer_rsrc(src + kv_base + (int64_t)key0 * kD, bytes);
     const uint32_t *off = plane == 0 ? k_off : v_off;
     const uint32_t base =
-        ring_base + (uint32_t)((((blk & 1) * 2 + plane) * kUnits + wave * 64) * 16);
+        ring_base + (uint32_t)(((((blk - first) & 1) * 2 + plane) * kUnits + wave * 64) * 16);
 #pragma unroll
     for (int p = 0; p < kLoads; ++p) {
       dma16(rs, off[p], base + (uint32_t)(p * kThreads * 16));
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
   /* S^T of block `blk` for this wave: keys 32*kt + (row), queries of tile
    * qt; one K operand read feeds all query tiles. */
   auto scores = [&](int blk, Scores &st) {
-    const u32x4 *kl = ring[blk & 1][0];
+    const u32x4 *kl = ring[(blk - first) & 1][0];
 #pragma unroll
     for (int ds = 0; ds < kDSteps; ++ds) {
 #pragma unroll
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
         }
       }
     }
-    const VX_LDS char *vl = (const VX_LDS char *)&ring[blk & 1][1][0];
+    const VX_LDS char *vl = (const VX_LDS char *)&ring[(blk - first) & 1][1][0];
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
 #pragma unroll
@@ -709,22 +711,22 @@ void launch(const uint16_t *q, const uint16_t *k, const uint16_t *v,
 std::atomic<int> forced_splits{0};
 
 /* Key splits for a launch: the query blocks alone give `items` workgroups.
- * Below one round of two per CU, and with at least 16 key blocks, the key
- * range is cut so that about one such round runs: at least 8 key blocks per
- * split, at most 8 splits (measured on the 512-query prefill chunks over
- * 2048 and 8192 keys: 4 splits of 128 items fastest, 6 and 8 slower; no
- * split pays over 512 keys). */
+ * Below one round of two per CU, the key range is cut so that about one such
+ * round runs, with at least 16 key blocks per split and at most 8 splits
+ * (measured on the 512-query prefill chunks, 128 items: over 2048 keys 2
+ * splits 35.5 us against 37.6 for 4; over 8192 keys 4 splits 88.8 us against
+ * 100.7 for 2 and 98-101 for 6 and 8; over 512 keys no split pays). */
 int pick_splits(int64_t items, int64_t key_blocks, int cus) {
   const int forced = forced_splits.load();
   if (forced > 0) {
     return (int)std::min<int64_t>(forced, std::max<int64_t>(key_blocks, 1));
   }
   const int64_t slots = 2 * (int64_t)cus;
-  if (items >= slots || key_blocks < 16) {
+  if (items >= slots) {
     return 1;
   }
   const int64_t want = (slots + items - 1) / items;
-  return (int)std::max<int64_t>(1, std::min<int64_t>({want, 8, key_blocks / 8}));
+  return (int)std::max<int64_t>(1, std::min<int64_t>({want, 8, key_blocks / 16}));
 }
 
 /* Split partials of one (device, stream). Launches on one stream run in
