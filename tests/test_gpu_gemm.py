@@ -232,9 +232,13 @@ def test_bf16_out_and_f16(hiplib, rng):
     assert_max_abs(c, exact, 1e-3, "f16 -> f32")
 
 
-@pytest.mark.parametrize("shape", [(37, 29, 53), (1, 768, 64), (300, 64, 257), (2, 3, 4)])
+@pytest.mark.parametrize("shape", [(37, 29, 53), (1, 768, 64), (300, 64, 257), (2, 3, 4),
+                                   (65, 100, 70)])
 @pytest.mark.parametrize("dt", [abi.DTYPE_F32, abi.DTYPE_BF16, abi.DTYPE_F64])
 def test_ragged_shapes(hiplib, shape, dt, rng):
+    """Exact-order kernel, bit-equal to the oracle: K under one step, one or
+    many whole steps, and whole steps followed by a partial one (K = 100:
+    one 64-deep f32 step plus 36; three 32-deep f64 steps plus 4)."""
     announce(f"gemm ragged {shape} dtype {dt}")
     m, k, n = shape
     a = rng.uniform(-1, 1, (m, k))
