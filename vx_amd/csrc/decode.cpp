@@ -101,11 +101,10 @@ bool ensure_io(LlamaI8 &m, int n_prompt, int n_out) {
   return true;
 }
 
-vxk::StepArgmaxArgs argmax_args(LlamaI8 &m, int n_prompt) {
-  vxk::StepArgmaxArgs a;
-  a.logits = m.logits;
-  a.vocab = m.cfg.vocab_size;
-  a.pos = m.pos;
+vxk::StepTokenArgs token_args(LlamaI8 &m, int n_prompt) {
+  vxk::StepTokenArgs a;
+  a.cand = m.best;
+  a.ncand = vxk::step_logits_groups(m.cfg.vocab_size);
   a.prompt = m.prompt;
   a.n_prompt = n_prompt;
   a.out_tokens = m.out_tokens;
@@ -113,12 +112,14 @@ vxk::StepArgmaxArgs argmax_args(LlamaI8 &m, int n_prompt) {
   a.out_cap = m.out_cap;
   a.tok_q = m.tok_q;
   a.tok_s = m.tok_s;
-  a.x = m.x;
-  a.dim = m.cfg.dim;
-  a.rope = m.rope;
-  a.rope_now = m.rope_now;
-  a.hs = m.hs;
-  a.seq_len = m.cfg.seq_len;
+  a.vocab = m.cfg.vocab_size;
+  return a;
+}
+
+vxk::StepArgmaxArgs argmax_args(LlamaI8 &m, int n_prompt) {
+  vxk::StepArgmaxArgs a;
+  a.tok = token_args(m, n_prompt);
+  a.pos = m.pos;
   return a;
 }
 
@@ -145,7 +146,17 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     qkv.x = m.x;
     qkv.norm = m.rms_att + (int64_t)l * c.dim;
     qkv.out = m.q;
-    vxk::step_gemv_qkv(qkv, m.stream);
+    if (l == 0) {
+      /* the position's token and its embedding as x; the rotary row */
+      qkv.tok = token_args(m, n_prompt);
+      qkv.xout = m.x;
+      qkv.rope_table = m.rope;
+      qkv.rope_out = m.rope_now;
+      qkv.seq_len = c.seq_len;
+      vxk::step_gemv_embed(qkv, m.stream);
+    } else {
+      vxk::step_gemv_qkv(qkv, m.stream);
+    }
 
     vxk::StepAttnArgs at;
     at.q = m.q;
@@ -198,8 +209,6 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
   lg.pos = m.pos;
   lg.part = m.best;
   vxk::step_gemv_logits(lg, m.stream);
-  vxk::step_choose_launch(argmax_args(m, n_prompt), m.best,
-                          vxk::step_logits_groups(c.vocab_size), m.stream);
 }
 
 } // namespace
@@ -353,6 +362,8 @@ int32_t vx_llama_i8_generate(void *model, const int32_t *prompt,
       enqueue_step(*m, n_prompt);
     }
   }
+  /* the token after the last step */
+  vxk::step_record_launch(start, m->stream);
   VX_HIP_CHECK(hipGetLastError());
   VX_HIP_CHECK(hipMemcpyAsync(out_tokens, m->out_tokens,
                               sizeof(int) * n_steps, hipMemcpyDeviceToHost,

@@ -2,9 +2,15 @@
  * decode.hip -- the GPU-resident token step of a Llama-2-style int8 decoder
  * (the semantics of reference examples/llama.vx:145-420).
  *
- * A step is 5 launches per layer plus 2, each reading the position from
+ * A step is 5 launches per layer plus 1, each reading the position from
  * device memory so that a captured step replays unchanged:
  *
+ *   step_gemv<kEmbed>  (layer 0) the position's token: the prompt's, or the
+ *                      argmax of the previous step's classifier candidates
+ *                      (lowest index wins a tie), recorded from the end of
+ *                      the prompt on; x = that token's embedding row, and
+ *                      the rotary row read at pos (and stored for the other
+ *                      layers); then as kQkv
  *   step_gemv<kQkv>    RMSNorm(x), [Wq; Wk; Wv] int8 GEMV, RoPE on
  *                      q and k, k and v into the KV cache at `pos`
  *   step_attention     kAttnSplit workgroups per head, each over every
@@ -18,10 +24,10 @@
  *   step_gemv<kResid>  x += W2 h
  *   step_gemv<kLogits> final RMSNorm, classifier (the embedding table);
  *                      each workgroup also leaves the best and runner-up of
- *                      its rows
- *   step_choose        merges those: argmax (lowest index wins a tie) or the
- *                      next prompt token; x = embedding of that token;
- *                      pos += 1
+ *                      its rows; pos += 1
+ *
+ * step_start sets up position 0 and step_record records the token that
+ * follows the last step.
  *
  * Every GEMV is weight-only int8 with one f32 scale per row over f32
  * activations (as in the reference, which is f32 throughout), f32 sums;
@@ -135,17 +141,38 @@ __device__ float block_max(float v, float *scratch) {
 using Best = StepBest;
 
 __device__ __forceinline__ Best merge(Best a, Best b) {
+  /* selects, not branches: a merge needs no wait on loads it does not use */
+  const bool bw = (b.v1 > a.v1) | ((b.v1 == a.v1) & (b.i1 < a.i1));
   Best r;
-  if (b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1)) {
-    r.v1 = b.v1;
-    r.i1 = b.i1;
-    r.v2 = fmaxf(a.v1, b.v2);
-  } else {
-    r.v1 = a.v1;
-    r.i1 = a.i1;
-    r.v2 = fmaxf(a.v2, b.v1);
-  }
+  r.v1 = bw ? b.v1 : a.v1;
+  r.i1 = bw ? b.i1 : a.i1;
+  r.v2 = bw ? fmaxf(a.v1, b.v2) : fmaxf(a.v2, b.v1);
   return r;
+}
+
+
+/* The better of a and its partner lane's Best (kO = 1, 2, 4, 8: within a
+ * 16-lane row by DPP; 16, 32: across rows by v_permlane16/32_swap, which
+ * hands each lane both halves' values, so merging the two gives the pair's
+ * result in either order). */
+template <int kO> __device__ __forceinline__ Best best_xchg(Best b) {
+  if constexpr (kO <= 8) {
+    Best o;
+    o.v1 = partner<kO>(b.v1);
+    o.i1 = __float_as_int(partner<kO>(__int_as_float(b.i1)));
+    o.v2 = partner<kO>(b.v2);
+    return merge(b, o);
+  } else {
+    auto sw = [](uint32_t x) {
+      return kO == 16 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                      : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    };
+    const auto v1 = sw(__float_as_uint(b.v1));
+    const auto i1 = sw((uint32_t)b.i1);
+    const auto v2 = sw(__float_as_uint(b.v2));
+    return merge(Best{__uint_as_float(v1[0]), (int)i1[0], __uint_as_float(v2[0])},
+                 Best{__uint_as_float(v1[1]), (int)i1[1], __uint_as_float(v2[1])});
+  }
 }
 
 
@@ -170,7 +197,12 @@ __device__ void logits_best(const StepGemvArgs &a, Best b) {
   }
 }
 
-enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4 };
+enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4, kEmbed = 5 };
+
+/* Classifier candidates each thread of the kEmbed GEMV requests before the
+ * weights (4 x 256 threads: vocabularies up to 32768 with 16 rows per
+ * candidate); any further ones are read after them. */
+constexpr int kEmbedCand = 4;
 
 /* Row pairs per wave: the classifier's waves take several, so its
  * thousands of rows need fewer workgroups (one round over the CUs). */
@@ -218,6 +250,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   const int r0 = pair0 * 2; /* the first (for kPairs == 1, the only) pair */
   const bool live = r0 < a.rows;
   constexpr bool kRes = kMode == kResid || kMode == kAttnResid;
+  constexpr bool kQkvLike = kMode == kQkv || kMode == kEmbed;
 
   /* Every load is a buffer load whose offset points past its range where
    * the element does not exist (zeros come back), so no branch surrounds a
@@ -242,6 +275,32 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
    * (max, sum) pairs of the column's head, two splits per load. */
   float ov[kMode == kAttnResid ? kAttnSplit : 1][kPer];
   u32x4 ml[kMode == kAttnResid ? kPer : 1][kAttnSplit / 2];
+  /* kEmbed: the previous classifier's candidates first (kEmbedCand per
+   * thread; a slot past ncand loads zeros and is replaced by an empty
+   * Best); the position and the prompt's token at it once the weights are
+   * requested (the prompt index waits for the position); the embedding row,
+   * which waits for the choice, last. */
+  constexpr int kCand = kMode == kEmbed ? kEmbedCand : 1;
+  float cv1[kCand], cv2[kCand];
+  int ci1[kCand];
+  int pos = 0;
+  int ptok = 0;
+  if constexpr (kMode == kEmbed) {
+    const int ncand = a.tok.ncand;
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.tok.cand, (short)0, ncand * (int)sizeof(Best), 0x00020000);
+#pragma unroll
+    for (int c = 0; c < kCand; ++c) {
+      const int j = t + c * kThreads;
+      const bool ok = j < ncand;
+      const uint32_t off = (uint32_t)(j * (int)sizeof(Best));
+      cv1[c] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(cr, (int)(ok ? off : kOut), 0, 0));
+      ci1[c] = (int)__builtin_amdgcn_raw_buffer_load_b32(cr, (int)(ok ? off + 4 : kOut), 0, 0);
+      cv2[c] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(cr, (int)(ok ? off + 8 : kOut), 0, 0));
+    }
+  }
   if constexpr (kMode == kAttnResid) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -259,7 +318,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
             xr, (int)(ok ? mo + 16 * q : kOut), 0, 0);
       }
     }
-  } else {
+  } else if constexpr (kMode != kEmbed) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int i = t + k * kThreads;
@@ -304,6 +363,12 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     sc1[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         sr, (int)(ok_r ? (uint32_t)(r * 4 + 4) : kOut), 0, 0));
   }
+  if constexpr (kMode == kEmbed) {
+    /* keep the position's round trip behind every weight request */
+    __builtin_amdgcn_sched_barrier(0);
+    pos = *a.pos;
+    ptok = a.tok.prompt[min(pos, a.tok.n_prompt - 1)]; /* clamped: no branch */
+  }
   float res0 = 0.0f, res1 = 0.0f;
   if constexpr (kRes) {
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
@@ -320,20 +385,28 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   }
 
   /* The rotary factors of this wave's (even, odd) pair at this step's
-   * position: step_choose (step_start at position 0) leaves that row of the
-   * table in a.rope, so they are requested behind the weights without
-   * waiting for the position. */
-  float fcr = 0.0f, fci = 0.0f;
-  int pos = 0;
-  if constexpr (kMode == kQkv) {
+   * position. Layer 0 (kEmbed) reads them from the table at pos, which it
+   * loaded first, and workgroup 0 also takes the whole row (ropev) to store
+   * it for the other layers, whose a.rope then holds it: those request
+   * theirs behind the weights without waiting for the position. */
+  float fcr = 0.0f, fci = 0.0f, ropev = 0.0f;
+  if constexpr (kQkvLike) {
+    const bool embed = kMode == kEmbed;
+    const int row0 = embed ? pos * a.hs : 0; /* first float of the row */
     const __amdgpu_buffer_rsrc_t ropr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)a.rope, (short)0, a.hs * 4, 0x00020000);
+        (void *)(embed ? a.rope_table : a.rope), (short)0,
+        (embed ? a.seq_len : 1) * a.hs * 4, 0x00020000);
     const int i = r0 < a.dim ? r0 : r0 - a.dim;
     const bool rot = live && r0 < a.dim + a.kv_dim;
-    const uint32_t roff = rot ? (uint32_t)((i % a.hs) * 4) : kOut;
+    const uint32_t roff = rot ? (uint32_t)((row0 + i % a.hs) * 4) : kOut;
     fcr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ropr, (int)roff, 0, 0));
     fci = __uint_as_float(
         __builtin_amdgcn_raw_buffer_load_b32(ropr, (int)(rot ? roff + 4 : kOut), 0, 0));
+    if constexpr (embed) {
+      const bool mine = blockIdx.x == 0 && t < a.hs;
+      ropev = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          ropr, (int)(mine ? (uint32_t)((row0 + t) * 4) : kOut), 0, 0));
+    }
   }
   if constexpr (kMode == kResid) {
 #pragma unroll
@@ -373,6 +446,69 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       xin[i] = num / den;
     }
   } else {
+    if constexpr (kMode == kEmbed) {
+      /* This position's token: the merge of the candidates (every thread
+       * ends with the same Best: the waves exchange theirs through LDS and
+       * each thread merges them in the same order). */
+      __shared__ Best wb[kThreads / 64];
+      Best b{-INFINITY, 0x7fffffff, -INFINITY};
+#pragma unroll
+      for (int c = 0; c < kCand; ++c) {
+        const bool ok = t + c * kThreads < a.tok.ncand;
+        b = merge(b, Best{ok ? cv1[c] : -INFINITY, ok ? ci1[c] : 0x7fffffff,
+                          ok ? cv2[c] : -INFINITY});
+      }
+      for (int j = t + kCand * kThreads; j < a.tok.ncand; j += kThreads) {
+        b = merge(b, a.tok.cand[j]);
+      }
+      b = best_xchg<1>(b);
+      b = best_xchg<2>(b);
+      b = best_xchg<4>(b);
+      b = best_xchg<8>(b);
+      b = best_xchg<16>(b);
+      b = best_xchg<32>(b);
+      if (lane == 0) {
+        wb[wave] = b;
+      }
+      __syncthreads();
+      Best r = wb[0];
+#pragma unroll
+      for (int w = 1; w < kThreads / 64; ++w) {
+        r = merge(r, wb[w]);
+      }
+      const bool prompt = pos < a.tok.n_prompt;
+      if (blockIdx.x == 0 && t == 0 && !prompt) {
+        const int at = pos - a.tok.n_prompt;
+        if (at < a.tok.out_cap) {
+          a.tok.out_tokens[at] = r.i1;
+          a.tok.out_margin[at] = r.v1 - r.v2;
+        }
+      }
+      /* Every logit NaN leaves no winner (index 0x7fffffff): read row 0
+       * rather than past the table; the NaN margin reports it. */
+      int tok = prompt ? ptok : r.i1;
+      tok = tok >= 0 && tok < a.tok.vocab ? tok : 0;
+      tok = __builtin_amdgcn_readfirstlane(tok);
+      const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)(a.tok.tok_q + (int64_t)tok * cols), (short)0, cols, 0x00020000);
+      const float es = a.tok.tok_s[tok];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int i = t + k * kThreads;
+        const int8_t e = (int8_t)__builtin_amdgcn_raw_buffer_load_b8(
+            er, (int)(i < cols ? (uint32_t)i : kOut), 0, 0);
+        xv[k] = (float)e * es;
+      }
+      if (blockIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int i = t + k * kThreads;
+          if (i < cols) {
+            a.xout[i] = xv[k];
+          }
+        }
+      }
+    }
     /* RMSNorm as reference examples/llama.vx:145-158. */
     if constexpr (kMode == kQkv) {
       pos = *a.pos; /* where k and v go in the cache */
@@ -436,8 +572,18 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     }
   }
   if constexpr (kMode == kLogits) {
+    /* The next step's position: a vector atomic, nothing waits for it (no
+     * other workgroup of this launch reads pos). */
+    if (blockIdx.x == 0 && t == 0) {
+      atomicAdd(a.pos, 1);
+    }
     logits_best(a, best);
     return;
+  }
+  if constexpr (kMode == kEmbed) {
+    if (blockIdx.x == 0 && t < a.hs) {
+      a.rope_out[t] = ropev;
+    }
   }
   if (lane != 0 || !live) {
     return;
@@ -445,7 +591,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   const float y0 = sc0[0] * acc0;
   const float y1 = sc1[0] * acc1;
 
-  if constexpr (kMode == kQkv) {
+  if constexpr (kQkvLike) {
     const int dim = a.dim, kv_dim = a.kv_dim;
     if (r0 < dim + kv_dim) {
       /* RoPE on the (even, odd) pair (reference :235-264). */
@@ -896,57 +1042,18 @@ __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) 
 
 constexpr int kChooseThreads = 1024;
 
-/* The better of a and its partner lane's Best (kO = 1, 2, 4, 8: within a
- * 16-lane row by DPP; 16, 32: across rows by v_permlane16/32_swap, which
- * hands each lane both halves' values, so merging the two gives the pair's
- * result in either order). */
-template <int kO> __device__ __forceinline__ Best best_xchg(Best b) {
-  if constexpr (kO <= 8) {
-    Best o;
-    o.v1 = partner<kO>(b.v1);
-    o.i1 = __float_as_int(partner<kO>(__int_as_float(b.i1)));
-    o.v2 = partner<kO>(b.v2);
-    return merge(b, o);
-  } else {
-    auto sw = [](uint32_t x) {
-      return kO == 16 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
-                      : __builtin_amdgcn_permlane32_swap(x, x, false, false);
-    };
-    const auto v1 = sw(__float_as_uint(b.v1));
-    const auto i1 = sw((uint32_t)b.i1);
-    const auto v2 = sw(__float_as_uint(b.v2));
-    return merge(Best{__uint_as_float(v1[0]), (int)i1[0], __uint_as_float(v2[0])},
-                 Best{__uint_as_float(v1[1]), (int)i1[1], __uint_as_float(v2[1])});
-  }
-}
-
-/* Merge the classifier workgroups' partials: argmax with the lowest index
- * winning a tie (reference examples/llama.vx:160-171), or the next prompt
- * token while the prompt lasts; then x = the embedding of that token and
- * pos + 1. The candidates and the position are requested first (they
- * depend on nothing), what the position selects (the prompt token, the
- * next step's rotary row) as soon as it arrives, so those round trips
- * overlap the reduction; only the embedding row waits for the choice. */
-__global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
-                                                              const Best *part,
-                                                              int nparts) {
+/* The token after the last step: the argmax of the last classifier's
+ * candidates (lowest index wins a tie, reference examples/llama.vx:160-171),
+ * recorded for position *pos, which the last classifier moved past the
+ * prompt; the steps themselves record the tokens before it. */
+__global__ __launch_bounds__(kChooseThreads) void step_record(StepArgmaxArgs a) {
   __shared__ Best merged[kChooseThreads / 64];
-  __shared__ int chosen;
   const int t = threadIdx.x;
   const int lane = t & 63;
-  /* this thread's first candidate in a register (a merge here would wait
-   * for it before the position is requested) */
-  Best b = t < nparts ? part[t] : Best{-INFINITY, 0x7fffffff, -INFINITY};
-  const int pos = *a.pos;
-  /* The next step's row of the rotary table (pairs for every head offset);
-   * none past the cache, where no step follows. */
-  const bool next_row = pos + 1 < a.seq_len;
-  const float rope0 =
-      next_row && t < a.hs ? a.rope[(int64_t)(pos + 1) * a.hs + t] : 0.0f;
-  const int prompt_tok =
-      t == 0 && pos + 1 < a.n_prompt ? a.prompt[pos + 1] : 0;
-  for (int i = t + kChooseThreads; i < nparts; i += kChooseThreads) {
-    b = merge(b, part[i]);
+  const int nparts = a.tok.ncand;
+  Best b{-INFINITY, 0x7fffffff, -INFINITY};
+  for (int i = t; i < nparts; i += kChooseThreads) {
+    b = merge(b, a.tok.cand[i]);
   }
   b = best_xchg<1>(b);
   b = best_xchg<2>(b);
@@ -963,51 +1070,17 @@ __global__ __launch_bounds__(kChooseThreads) void step_choose(StepArgmaxArgs a,
     for (int w = 1; w < kChooseThreads / 64; ++w) {
       r = merge(r, merged[w]);
     }
-    int tok;
-    if (pos + 1 < a.n_prompt) {
-      tok = prompt_tok;
-    } else {
-      tok = r.i1;
-      const int at = pos + 1 - a.n_prompt;
-      if (at < a.out_cap) {
-        a.out_tokens[at] = tok;
-        a.out_margin[at] = r.v1 - r.v2;
-      }
+    const int pos = *a.pos;
+    const int at = pos - a.tok.n_prompt;
+    if (at >= 0 && at < a.tok.out_cap) {
+      a.tok.out_tokens[at] = r.i1;
+      a.tok.out_margin[at] = r.v1 - r.v2;
     }
-    /* Every logit NaN leaves no winner (index 0x7fffffff): read row 0
-     * rather than past the table; the NaN margin reports it. */
-    chosen = tok >= 0 && tok < a.vocab ? tok : 0;
-  }
-  __syncthreads();
-  const int tok = chosen;
-  const float s = a.tok_s[tok];
-  for (int i = t; i < a.dim; i += kChooseThreads) {
-    a.x[i] = (float)a.tok_q[(int64_t)tok * a.dim + i] * s;
-  }
-  if (next_row) {
-    if (t < a.hs) {
-      a.rope_now[t] = rope0;
-    }
-    for (int i = t + kChooseThreads; i < a.hs; i += kChooseThreads) {
-      a.rope_now[i] = a.rope[(int64_t)(pos + 1) * a.hs + i];
-    }
-  }
-  if (t == 0) {
-    *a.pos = pos + 1;
   }
 }
 
-/* Position 0: the first prompt token's embedding and row 0 of the rotary
- * table. */
+/* Position 0; layer 0 of the first step reads its token and rotary row. */
 __global__ void step_start(StepArgmaxArgs a) {
-  for (int i = threadIdx.x; i < a.hs; i += blockDim.x) {
-    a.rope_now[i] = a.rope[i];
-  }
-  const int tok = a.prompt[0];
-  const float s = a.tok_s[tok];
-  for (int i = threadIdx.x; i < a.dim; i += blockDim.x) {
-    a.x[i] = (float)a.tok_q[(int64_t)tok * a.dim + i] * s;
-  }
   if (threadIdx.x == 0) {
     *a.pos = 0;
   }
@@ -1040,6 +1113,7 @@ bool step_gemv_ok(int rows, int cols) {
 }
 
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kQkv>(a, s); }
+void step_gemv_embed(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kEmbed>(a, s); }
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kResid>(a, s); }
 void step_gemv_attn_resid(const StepGemvArgs &a, hipStream_t s) {
   launch_gemv<kAttnResid>(a, s);
@@ -1049,10 +1123,8 @@ void step_gemv_logits(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kLogit
 
 int step_logits_groups(int rows) { return gemv_groups<kLogits>(rows); }
 
-void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
-                        int nparts, hipStream_t s) {
-  hipLaunchKernelGGL(step_choose, dim3(1), dim3(kChooseThreads), 0, s, a, part,
-                     nparts);
+void step_record_launch(const StepArgmaxArgs &a, hipStream_t s) {
+  hipLaunchKernelGGL(step_record, dim3(1), dim3(kChooseThreads), 0, s, a);
 }
 
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
@@ -1072,7 +1144,7 @@ void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
 }
 
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(step_start, dim3(1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(step_start, dim3(1), dim3(64), 0, s, a);
 }
 
 } // namespace vxk

@@ -12,31 +12,33 @@
 
 namespace vxk {
 
-struct StepArgmaxArgs {
-  const float *logits;
-  int vocab;
-  int *pos;
-  const int *prompt;
-  int n_prompt;
-  int *out_tokens;
-  float *out_margin;
-  int out_cap;
-  const int8_t *tok_q;
-  const float *tok_s;
-  float *x;
-  int dim;
-  /* The rotary table [seq_len, hs/2, 2] and the row of it for the next
-   * step, which the QKV GEMVs read. */
-  const float *rope;
-  float *rope_now;
-  int hs, seq_len;
-};
-
 /* Best and runner-up logit of a workgroup's rows (classifier epilogue). */
 struct StepBest {
   float v1;
   int i1;
   float v2;
+};
+
+/* The token of a position: the prompt's while it lasts, else the argmax
+ * over the previous step's classifier candidates (lowest index on a tie),
+ * recorded in out_tokens / out_margin from position n_prompt on. */
+struct StepTokenArgs {
+  const StepBest *cand; /* ncand entries left by the previous classifier */
+  int ncand;
+  const int *prompt;
+  int n_prompt;
+  int *out_tokens;
+  float *out_margin;
+  int out_cap;
+  const int8_t *tok_q; /* embedding table [vocab, dim], int8 rows */
+  const float *tok_s;  /* and their scales */
+  int vocab;
+};
+
+/* Position 0 (step_start) and the token after the last step (step_record). */
+struct StepArgmaxArgs {
+  StepTokenArgs tok;
+  int *pos;
 };
 
 struct StepGemvArgs {
@@ -51,10 +53,19 @@ struct StepGemvArgs {
   float *hout;         /* SwiGLU output */
   float *kcache, *vcache; /* this layer's [seq, kv_dim] */
   const float *rope;   /* this step's row of the rotary table: [hs/2, 2] */
-  const int *pos;
+  int *pos;            /* the classifier advances it; the rest only read it */
   int dim, kv_dim, hs;
   /* Classifier only: one StepBest per workgroup. */
   StepBest *part;
+  /* Layer 0's QKV GEMV (step_gemv_embed): the token of this position, whose
+   * embedding row is the input (also stored to xout), and the rotary table
+   * [seq_len, hs/2, 2], read at pos directly and whose row it stores to
+   * rope_out for the other layers. */
+  StepTokenArgs tok;
+  float *xout;
+  const float *rope_table;
+  float *rope_out;
+  int seq_len;
 };
 
 /* Workgroups per head in step_attention: split s takes positions s,
@@ -86,19 +97,24 @@ struct StepAttnArgs {
 /* rows even, cols a multiple of 16 and at most 4096. */
 bool step_gemv_ok(int rows, int cols);
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s);
+/* Layer 0's QKV GEMV: picks the position's token (a.tok) and reads its
+ * embedding row instead of a.x. */
+void step_gemv_embed(const StepGemvArgs &a, hipStream_t s);
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s);
 /* x += Wo merge(attention partials); cols = heads * hs, hs dividing cols. */
 void step_gemv_attn_resid(const StepGemvArgs &a, hipStream_t s);
 void step_gemv_swiglu(const StepGemvArgs &a, hipStream_t s);
 /* The classifier; leaves step_logits_groups(rows) StepBest entries in
- * `part` for step_choose_launch. */
+ * `part` for the next step's token (step_gemv_embed, or step_record after
+ * the last step), and moves pos on by one. */
 void step_gemv_logits(const StepGemvArgs &a, hipStream_t s);
 int step_logits_groups(int rows);
-void step_choose_launch(const StepArgmaxArgs &a, const StepBest *part,
-                        int nparts, hipStream_t s);
+/* Records the token of position *pos (after the last step). */
+void step_record_launch(const StepArgmaxArgs &a, hipStream_t s);
 /* hs divides 256 and is at most 256; seq_len * 4 bytes of LDS. */
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
                            hipStream_t s);
+/* pos = 0. */
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s);
 
 } // namespace vxk
