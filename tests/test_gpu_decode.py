@@ -71,6 +71,47 @@ def test_tiny_greedy_stream_matches_oracle(hiplib, graph):
     np.testing.assert_allclose(gm, margin, atol=1e-3)
 
 
+@pytest.mark.parametrize("n_prompt", [1, 6])
+def test_single_step_and_single_token_prompt(hiplib, n_prompt):
+    """One step: the only token is the one recorded after the last prompt
+    position; a one-token prompt: the first step already reads candidates
+    (position 1 on)."""
+    announce(f"decode one step, prompt {n_prompt}")
+    cfg = CONFIG_TINY
+    weights = make_model(cfg, seed=3)
+    prompt = make_prompt(cfg, n=n_prompt, seed=5)
+    want, margin = oracle.llama_generate(cfg.as_dict(), weights, prompt, 8)
+    model = LlamaI8(hiplib, cfg, weights)
+    for graph in (True, False):
+        got, gm = model.generate(prompt, 1, graph=graph)
+        assert int(got[0]) == int(want[0]), f"graph={graph}"
+        np.testing.assert_allclose(gm[:1], margin[:1], atol=1e-3)
+        got, gm = model.generate(prompt, 8, graph=graph)
+        assert_same_tokens(got, want, margin)
+    model.close()
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_large_vocab_greedy_stream_matches_oracle(hiplib, graph):
+    """A vocabulary of 40000 leaves 1250 classifier candidates, more than the
+    1024 that layer 0's token choice requests before its weights: the rest
+    go through its second loop. The prompt ends on token 39001, so the
+    first choices are won by a row that only those candidates cover."""
+    announce(f"decode vocab 40000 greedy graph={graph}")
+    cfg = LlamaConfig(dim=64, hidden_dim=128, n_layers=2, n_heads=4, n_kv_heads=2,
+                      vocab_size=40000, seq_len=64)
+    weights = make_model(cfg, seed=3)
+    prompt = make_prompt(cfg, n=6, seed=5)
+    prompt[-1] = 39001
+    want, margin = oracle.llama_generate(cfg.as_dict(), weights, prompt, 40)
+    assert any(int(t) >= 32768 for t in want)  # rows of candidates 1024 and up
+    model = LlamaI8(hiplib, cfg, weights)
+    got, gm = model.generate(prompt, 40, graph=graph)
+    model.close()
+    assert_same_tokens(got, want, margin)
+    np.testing.assert_allclose(gm, margin, atol=1e-3)
+
+
 def test_config4_greedy_stream_matches_oracle(hiplib):
     """BASELINE config 4, 16-token prompt, 256 greedy tokens: the same stream
     as the CPU oracle (tests/golden/make_decode_golden.py)."""

@@ -148,12 +148,13 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     qkv.out = m.q;
     if (l == 0) {
       /* the position's token and its embedding as x; the rotary row */
-      qkv.tok = token_args(m, n_prompt);
-      qkv.xout = m.x;
-      qkv.rope_table = m.rope;
-      qkv.rope_out = m.rope_now;
-      qkv.seq_len = c.seq_len;
-      vxk::step_gemv_embed(qkv, m.stream);
+      vxk::StepEmbedArgs e;
+      e.tok = token_args(m, n_prompt);
+      e.xout = m.x;
+      e.rope_table = m.rope;
+      e.rope_out = m.rope_now;
+      e.seq_len = c.seq_len;
+      vxk::step_gemv_embed(qkv, e, m.stream);
     } else {
       vxk::step_gemv_qkv(qkv, m.stream);
     }

@@ -236,7 +236,7 @@ template <int kMode> constexpr int pairs_per_wave() {
 /* kSegs: 1024-column segments the kernel is built for (cols <= 1024 kSegs),
  * so registers and LDS are sized to the matrix rather than to kMaxCols. */
 template <int kMode, int kSegs>
-__global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
+__device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbedArgs &e) {
 #pragma clang fp contract(off)
   constexpr int kCols = kSegs * 1024;
   __shared__ float xin[kCols];
@@ -286,9 +286,9 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   int pos = 0;
   int ptok = 0;
   if constexpr (kMode == kEmbed) {
-    const int ncand = a.tok.ncand;
+    const int ncand = e.tok.ncand;
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)a.tok.cand, (short)0, ncand * (int)sizeof(Best), 0x00020000);
+        (void *)e.tok.cand, (short)0, ncand * (int)sizeof(Best), 0x00020000);
 #pragma unroll
     for (int c = 0; c < kCand; ++c) {
       const int j = t + c * kThreads;
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     /* keep the position's round trip behind every weight request */
     __builtin_amdgcn_sched_barrier(0);
     pos = *a.pos;
-    ptok = a.tok.prompt[min(pos, a.tok.n_prompt - 1)]; /* clamped: no branch */
+    ptok = e.tok.prompt[min(pos, e.tok.n_prompt - 1)]; /* clamped: no branch */
   }
   float res0 = 0.0f, res1 = 0.0f;
   if constexpr (kRes) {
@@ -394,8 +394,8 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     const bool embed = kMode == kEmbed;
     const int row0 = embed ? pos * a.hs : 0; /* first float of the row */
     const __amdgpu_buffer_rsrc_t ropr = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(embed ? a.rope_table : a.rope), (short)0,
-        (embed ? a.seq_len : 1) * a.hs * 4, 0x00020000);
+        (void *)(embed ? e.rope_table : a.rope), (short)0,
+        (embed ? e.seq_len : 1) * a.hs * 4, 0x00020000);
     const int i = r0 < a.dim ? r0 : r0 - a.dim;
     const bool rot = live && r0 < a.dim + a.kv_dim;
     const uint32_t roff = rot ? (uint32_t)((row0 + i % a.hs) * 4) : kOut;
@@ -454,12 +454,12 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       Best b{-INFINITY, 0x7fffffff, -INFINITY};
 #pragma unroll
       for (int c = 0; c < kCand; ++c) {
-        const bool ok = t + c * kThreads < a.tok.ncand;
+        const bool ok = t + c * kThreads < e.tok.ncand;
         b = merge(b, Best{ok ? cv1[c] : -INFINITY, ok ? ci1[c] : 0x7fffffff,
                           ok ? cv2[c] : -INFINITY});
       }
-      for (int j = t + kCand * kThreads; j < a.tok.ncand; j += kThreads) {
-        b = merge(b, a.tok.cand[j]);
+      for (int j = t + kCand * kThreads; j < e.tok.ncand; j += kThreads) {
+        b = merge(b, e.tok.cand[j]);
       }
       b = best_xchg<1>(b);
       b = best_xchg<2>(b);
@@ -476,22 +476,22 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
       for (int w = 1; w < kThreads / 64; ++w) {
         r = merge(r, wb[w]);
       }
-      const bool prompt = pos < a.tok.n_prompt;
+      const bool prompt = pos < e.tok.n_prompt;
       if (blockIdx.x == 0 && t == 0 && !prompt) {
-        const int at = pos - a.tok.n_prompt;
-        if (at < a.tok.out_cap) {
-          a.tok.out_tokens[at] = r.i1;
-          a.tok.out_margin[at] = r.v1 - r.v2;
+        const int at = pos - e.tok.n_prompt;
+        if (at < e.tok.out_cap) {
+          e.tok.out_tokens[at] = r.i1;
+          e.tok.out_margin[at] = r.v1 - r.v2;
         }
       }
       /* Every logit NaN leaves no winner (index 0x7fffffff): read row 0
        * rather than past the table; the NaN margin reports it. */
       int tok = prompt ? ptok : r.i1;
-      tok = tok >= 0 && tok < a.tok.vocab ? tok : 0;
+      tok = tok >= 0 && tok < e.tok.vocab ? tok : 0;
       tok = __builtin_amdgcn_readfirstlane(tok);
       const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc(
-          (void *)(a.tok.tok_q + (int64_t)tok * cols), (short)0, cols, 0x00020000);
-      const float es = a.tok.tok_s[tok];
+          (void *)(e.tok.tok_q + (int64_t)tok * cols), (short)0, cols, 0x00020000);
+      const float es = e.tok.tok_s[tok];
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
         const int i = t + k * kThreads;
@@ -504,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
         for (int k = 0; k < kPer; ++k) {
           const int i = t + k * kThreads;
           if (i < cols) {
-            a.xout[i] = xv[k];
+            e.xout[i] = xv[k];
           }
         }
       }
@@ -582,7 +582,7 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
   }
   if constexpr (kMode == kEmbed) {
     if (blockIdx.x == 0 && t < a.hs) {
-      a.rope_out[t] = ropev;
+      e.rope_out[t] = ropev;
     }
   }
   if (lane != 0 || !live) {
@@ -622,6 +622,16 @@ __global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
     val = val * y1;
     a.hout[r0 >> 1] = val;
   }
+}
+
+template <int kMode, int kSegs>
+__global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
+  gemv_body<kMode, kSegs>(a, StepEmbedArgs{});
+}
+
+template <int kSegs>
+__global__ __launch_bounds__(kThreads) void step_gemv_embed(StepGemvArgs a, StepEmbedArgs e) {
+  gemv_body<kEmbed, kSegs>(a, e);
 }
 
 /* Workgroup (h, sp) of query head h over positions sp, sp + kAttnSplit,
@@ -1104,6 +1114,18 @@ void launch_gemv(const StepGemvArgs &a, hipStream_t s) {
   }
 }
 
+void launch_embed(const StepGemvArgs &a, const StepEmbedArgs &e, hipStream_t s) {
+  const dim3 grid(gemv_groups<kEmbed>(a.rows));
+  if (a.cols <= 1024) {
+    hipLaunchKernelGGL((step_gemv_embed<1>), grid, dim3(kThreads), 0, s, a, e);
+  } else if (a.cols <= 2048) {
+    hipLaunchKernelGGL((step_gemv_embed<2>), grid, dim3(kThreads), 0, s, a, e);
+  } else {
+    hipLaunchKernelGGL((step_gemv_embed<kMaxCols / 1024>), grid, dim3(kThreads), 0, s,
+                       a, e);
+  }
+}
+
 } // namespace
 
 bool step_gemv_ok(int rows, int cols) {
@@ -1113,7 +1135,9 @@ bool step_gemv_ok(int rows, int cols) {
 }
 
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kQkv>(a, s); }
-void step_gemv_embed(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kEmbed>(a, s); }
+void step_gemv_embed(const StepGemvArgs &a, const StepEmbedArgs &e, hipStream_t s) {
+  launch_embed(a, e, s);
+}
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s) { launch_gemv<kResid>(a, s); }
 void step_gemv_attn_resid(const StepGemvArgs &a, hipStream_t s) {
   launch_gemv<kAttnResid>(a, s);

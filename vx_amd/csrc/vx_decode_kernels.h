@@ -57,10 +57,14 @@ struct StepGemvArgs {
   int dim, kv_dim, hs;
   /* Classifier only: one StepBest per workgroup. */
   StepBest *part;
-  /* Layer 0's QKV GEMV (step_gemv_embed): the token of this position, whose
-   * embedding row is the input (also stored to xout), and the rotary table
-   * [seq_len, hs/2, 2], read at pos directly and whose row it stores to
-   * rope_out for the other layers. */
+};
+
+/* Layer 0's QKV GEMV (step_gemv_embed) also takes: the token of this
+ * position, whose embedding row is its input (also stored to xout), and the
+ * rotary table [seq_len, hs/2, 2], read at pos directly and whose row it
+ * stores to rope_out for the other layers. (A second argument of that one
+ * kernel, so that the other GEMVs' arguments stay small.) */
+struct StepEmbedArgs {
   StepTokenArgs tok;
   float *xout;
   const float *rope_table;
@@ -97,9 +101,9 @@ struct StepAttnArgs {
 /* rows even, cols a multiple of 16 and at most 4096. */
 bool step_gemv_ok(int rows, int cols);
 void step_gemv_qkv(const StepGemvArgs &a, hipStream_t s);
-/* Layer 0's QKV GEMV: picks the position's token (a.tok) and reads its
+/* Layer 0's QKV GEMV: picks the position's token (e.tok) and reads its
  * embedding row instead of a.x. */
-void step_gemv_embed(const StepGemvArgs &a, hipStream_t s);
+void step_gemv_embed(const StepGemvArgs &a, const StepEmbedArgs &e, hipStream_t s);
 void step_gemv_resid(const StepGemvArgs &a, hipStream_t s);
 /* x += Wo merge(attention partials); cols = heads * hs, hs dividing cols. */
 void step_gemv_attn_resid(const StepGemvArgs &a, hipStream_t s);
