@@ -177,8 +177,8 @@ template <int kO> __device__ __forceinline__ Best best_xchg(Best b) {
 
 
 /* Classifier epilogue: the best and runner-up of this workgroup's rows
- * (each wave's lane 0 holds its own in `b`) into part[blockIdx.x], for
- * step_choose to merge. */
+ * (each wave's lane 0 holds its own in `b`) into part[blockIdx.x], for the
+ * next step's token choice (step_gemv_embed, or step_record) to merge. */
 __device__ void logits_best(const StepGemvArgs &a, Best b) {
   __shared__ Best wbest[kThreads / 64];
   const int t = threadIdx.x;
