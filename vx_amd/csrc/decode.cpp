@@ -6,10 +6,10 @@
  * matrix: per layer [Wq; Wk; Wv] stacked (one GEMV feeds RoPE and the KV
  * cache) and W1/W3 interleaved row by row (one GEMV feeds SwiGLU). The
  * position and the next token live in device memory; a step is a fixed
- * sequence of 5 * layers + 2 launches that, with VX_LLAMA_GRAPH, is captured
- * once into a hipGraph (kept with the model while the prompt length and I/O
- * buffers stay the same) and replayed per token with no host
- * synchronisation until the tokens are read back.
+ * sequence of 5 * layers + 1 launches that, with VX_LLAMA_GRAPH, is captured
+ * into hipGraphs of kGraphSteps steps and of one step (kept with the model
+ * while the prompt length and I/O buffers stay the same) and replayed with
+ * no host synchronisation until the tokens are read back.
  */
 #include "../../include/vx_hardware_runtime.h"
 #include "../../include/vx_hip_ops.h"
@@ -21,6 +21,13 @@
 #include <vector>
 
 namespace {
+
+/* Steps per replay of the long graph (the positions left over go through
+ * the one-step graph). */
+#ifndef VX_DEC_GRAPH_STEPS
+#define VX_DEC_GRAPH_STEPS 8
+#endif
+constexpr int kGraphSteps = VX_DEC_GRAPH_STEPS;
 
 struct LlamaI8 {
   vx_llama_i8_config cfg;
@@ -39,10 +46,11 @@ struct LlamaI8 {
   vxk::StepBest *best = nullptr; /* one per classifier workgroup */
   int prompt_cap = 0, out_cap = 0;
   hipStream_t stream = nullptr;
-  /* The instantiated step graph, kept across generate calls: it bakes in
-   * the prompt length and the I/O buffers, so it is dropped when either
-   * changes. */
+  /* The instantiated step graphs (one step, kGraphSteps steps), kept across
+   * generate calls: they bake in the prompt length and the I/O buffers, so
+   * they are dropped when either changes. */
   hipGraphExec_t step_exec = nullptr;
+  hipGraphExec_t steps_exec = nullptr;
   int step_exec_prompt = -1;
   std::vector<void *> owned;
 };
@@ -62,9 +70,11 @@ template <typename T> T *alloc(LlamaI8 &m, size_t count) {
 }
 
 void drop_step_graph(LlamaI8 &m) {
-  if (m.step_exec) {
-    (void)hipGraphExecDestroy(m.step_exec);
-    m.step_exec = nullptr;
+  for (hipGraphExec_t *g : {&m.step_exec, &m.steps_exec}) {
+    if (*g) {
+      (void)hipGraphExecDestroy(*g);
+      *g = nullptr;
+    }
   }
   m.step_exec_prompt = -1;
 }
@@ -347,15 +357,29 @@ int32_t vx_llama_i8_generate(void *model, const int32_t *prompt,
   if (flags & VX_LLAMA_GRAPH) {
     if (!m->step_exec || m->step_exec_prompt != n_prompt) {
       drop_step_graph(*m);
-      hipGraph_t graph = nullptr;
-      VX_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
-      enqueue_step(*m, n_prompt);
-      VX_HIP_CHECK(hipStreamEndCapture(m->stream, &graph));
-      VX_HIP_CHECK(hipGraphInstantiate(&m->step_exec, graph, nullptr, nullptr, 0));
-      VX_HIP_CHECK(hipGraphDestroy(graph));
+      auto capture = [&](int steps) {
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        VX_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+        for (int i = 0; i < steps; ++i) {
+          enqueue_step(*m, n_prompt);
+        }
+        VX_HIP_CHECK(hipStreamEndCapture(m->stream, &graph));
+        VX_HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+        VX_HIP_CHECK(hipGraphDestroy(graph));
+        return exec;
+      };
+      m->step_exec = capture(1);
+      if (kGraphSteps > 1) {
+        m->steps_exec = capture(kGraphSteps);
+      }
       m->step_exec_prompt = n_prompt;
     }
-    for (int p = 0; p < positions; ++p) {
+    int p = 0;
+    for (; kGraphSteps > 1 && p + kGraphSteps <= positions; p += kGraphSteps) {
+      VX_HIP_CHECK(hipGraphLaunch(m->steps_exec, m->stream));
+    }
+    for (; p < positions; ++p) {
       VX_HIP_CHECK(hipGraphLaunch(m->step_exec, m->stream));
     }
   } else {
