@@ -71,6 +71,24 @@ def test_tiny_greedy_stream_matches_oracle(hiplib, graph):
     np.testing.assert_allclose(gm, margin, atol=1e-3)
 
 
+@pytest.mark.parametrize("cfg", [
+    # layer 0's token choice built for 2 and 4 column segments (rows of 1152 and 2304)
+    LlamaConfig(dim=1152, hidden_dim=3072, n_layers=1, n_heads=18, n_kv_heads=6,
+                vocab_size=512, seq_len=64),
+    LlamaConfig(dim=2304, hidden_dim=1024, n_layers=1, n_heads=18, n_kv_heads=6,
+                vocab_size=640, seq_len=48)])
+def test_wide_rows_greedy_stream_matches_oracle(hiplib, cfg):
+    announce(f"decode wide greedy {cfg}")
+    weights = make_model(cfg, seed=3)
+    prompt = make_prompt(cfg, n=5, seed=5)
+    want, margin = oracle.llama_generate(cfg.as_dict(), weights, prompt, 30)
+    model = LlamaI8(hiplib, cfg, weights)
+    got, gm = model.generate(prompt, 30)
+    model.close()
+    assert_same_tokens(got, want, margin)
+    np.testing.assert_allclose(gm, margin, atol=1e-3)
+
+
 @pytest.mark.parametrize("n_prompt", [1, 6])
 def test_single_step_and_single_token_prompt(hiplib, n_prompt):
     """One step: the only token is the one recorded after the last prompt
