@@ -78,6 +78,11 @@ KERNEL_CASES = [
     (abi.GEMV_LDS, (4096, 4096), 16), (abi.GEMV_LDS, (8200, 1040), 12),
     (abi.GEMV_LDS, (4096, 4096), 1), (abi.GEMV_LDS, (65, 272), 3),
     (abi.GEMV_LDS, (11008, 4096), 8), (abi.GEMV_LDS, (4096, 11008), 2),
+    # 16-row tiles at batches of 8 and more: 256 workgroups (x through LDS,
+    # one round on 256 CUs), 257 (x straight from L2), and x through LDS with
+    # a partial last tile and batch rows past nb
+    (abi.GEMV_LDS, (4096, 1040), 8), (abi.GEMV_LDS, (4099, 1040), 8),
+    (abi.GEMV_LDS, (100, 2064), 9),
 ]
 
 

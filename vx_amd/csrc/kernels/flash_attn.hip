@@ -761,21 +761,6 @@ bool reserve(SplitSpace &sp, size_t bytes, hipStream_t stream) {
   return true;
 }
 
-int device_cus() {
-  static std::atomic<int> cached{0};
-  int n = cached.load();
-  if (n == 0) {
-    int dev = 0;
-    hipDeviceProp_t prop;
-    n = hipGetDevice(&dev) == hipSuccess &&
-                hipGetDeviceProperties(&prop, dev) == hipSuccess
-            ? prop.multiProcessorCount
-            : 256;
-    cached.store(n);
-  }
-  return n;
-}
-
 } // namespace
 
 void flash_attn_force_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0); }
@@ -807,7 +792,7 @@ bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
   constexpr int kBlockQ = 4 * 32 * VX_FA_QT;
   const int64_t items = bh * ((seq_q + kBlockQ - 1) / kBlockQ);
   const int64_t key_blocks = (seq_k + VX_FA_BK - 1) / VX_FA_BK;
-  int splits = allow_split ? pick_splits(items, key_blocks, device_cus()) : 1;
+  int splits = allow_split ? pick_splits(items, key_blocks, device_cu_count()) : 1;
   /* Both grids stay within 32-bit workgroup and thread counts. */
   if (items * splits > INT32_MAX || bh * seq_q * (head_dim / 4) > INT32_MAX) {
     splits = 1;

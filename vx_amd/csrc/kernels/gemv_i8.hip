@@ -341,14 +341,27 @@ __device__ __forceinline__ f32x4 mfma_bf16(const uint32_t *a, u32x4 b, f32x4 c) 
  *
  * Loads retire in issue order, so each pass issues this tile's x loads,
  * then writes the tile (waiting for its weights), then issues the next
- * tile's weight loads, and only then waits for x: the prefetch stays in
- * flight through the multiply. Buffer loads return zero past the end of
- * their range, which covers the last rows, the last columns and the batch
- * rows past nb without a branch.
+ * tile's weight loads, and only then waits for x. Buffer loads return zero
+ * past the end of their range, which covers the last rows, the last columns
+ * and the batch rows past nb without a branch.
+ *
+ * kXl (16-row tiles): x goes through the wave's LDS as well. The wave
+ * loads its x columns as whole 128-byte lines of each batch row (in operand
+ * order a load instruction touches 16 half lines), writes them to an x
+ * tile beside the weight tile and reads the MFMA operands from there; and
+ * the next tile's weights are requested with no branch around the loads (a
+ * tile past the last has every column past `cols`), so the multiply waits
+ * for x alone (behind a branch the compiler's waits at the join count the
+ * prefetch as possibly absent, and each tile's last MFMA waited for it).
+ * The x tile makes a workgroup's LDS 100 KiB, one workgroup per CU, so the
+ * launch takes it only when the grid fits one round, and for batches of 8
+ * and more (below, most of the tile is zeros and its LDS round trip cost
+ * more than the whole lines saved). The branch-free prefetch alone, or on
+ * 64-row tiles, measured slower.
  *
  * Workgroup g owns rows 16 kR g ..; its kW waves take the column tiles w,
  * w + kW, ...; their accumulators meet in LDS at the end. */
-template <int kW, int kCols, int kR>
+template <int kW, int kCols, int kR, bool kXl>
 __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
     const int8_t *__restrict__ W, const float *__restrict__ scale,
     const uint16_t *__restrict__ X, float *__restrict__ Y, int rows, int cols,
@@ -360,13 +373,22 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
   constexpr int kInst = kRows / kRowsPerInst;
   constexpr int kSteps = kCols / 64;
   constexpr uint32_t kOut = 0x80000000u; /* past every range */
+  /* x tile (kXl): 16 batch rows of kCols bf16, rows padded by 16 bytes;
+   * each load instruction covers 64 * 16 bytes of it in whole lines. */
+  static_assert(!kXl || kR == 1, "x tiles are built for 16-row tiles");
+  constexpr int kXStride = kCols * 2 + 16;
+  constexpr int kXLanesPerRow = kCols * 2 / 16;
+  constexpr int kXRowsPerInst = 64 / kXLanesPerRow;
+  constexpr int kXInst = kXl ? 16 / kXRowsPerInst : 1;
+  constexpr int kWaveBytes = kRows * kStride + (kXl ? 16 * kXStride : 0);
+  static_assert(!kXl || (kXLanesPerRow <= 64 && 64 % kXLanesPerRow == 0), "x tile shape");
   /* The waves' tiles and, once every wave is past its last tile, the
    * partial sums share one LDS block. */
-  constexpr int kTileBytes = kW * kRows * kStride;
+  constexpr int kTileBytes = kW * kWaveBytes;
   constexpr int kRedBytes = kW * kRows * 17 * 4;
   __shared__ __attribute__((aligned(16)))
   int8_t smem[kTileBytes > kRedBytes ? kTileBytes : kRedBytes];
-  auto tile = reinterpret_cast<int8_t (*)[kRows * kStride]>(smem);
+  auto tile = reinterpret_cast<int8_t (*)[kWaveBytes]>(smem);
   auto red = reinterpret_cast<float (*)[kRows][17]>(smem);
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -381,6 +403,7 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       (void *)X, (short)0, nb * cols * 2, 0x00020000);
   int8_t *my = tile[wave];
+  int8_t *myx = my + kRows * kStride; /* kXl: this wave's x tile */
   const int ntiles = (cols + kCols - 1) / kCols;
 
   u32x4 cur[kInst];
@@ -398,19 +421,33 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
     acc[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
   u32x4 xa[kSteps], xb[kSteps];
+  u32x4 xl[kXInst];
   auto load_x = [&](int s) {
+    if constexpr (kXl) {
+      /* lane l of instruction i: batch row i * kXRowsPerInst + l /
+       * kXLanesPerRow, 8 columns at (l % kXLanesPerRow) * 8 */
+      const int c = s * kCols + (lane % kXLanesPerRow) * 8;
 #pragma unroll
-    for (int jj = 0; jj < kSteps; ++jj) {
-      const int c = s * kCols + 64 * jj + 8 * g;
-      const uint32_t off = (uint32_t)((m * cols + c) * 2);
-      xa[jj] = __builtin_amdgcn_raw_buffer_load_b128(
-          xr, (int)(m < nb && c < cols ? off : kOut), 0, 0);
-      xb[jj] = __builtin_amdgcn_raw_buffer_load_b128(
-          xr, (int)(m < nb && c + 32 < cols ? off + 64 : kOut), 0, 0);
+      for (int i = 0; i < kXInst; ++i) {
+        const int n = i * kXRowsPerInst + lane / kXLanesPerRow;
+        const uint32_t off = (uint32_t)((n * cols + c) * 2);
+        xl[i] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (int)(n < nb && c < cols ? off : kOut), 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < kSteps; ++jj) {
+        const int c = s * kCols + 64 * jj + 8 * g;
+        const uint32_t off = (uint32_t)((m * cols + c) * 2);
+        xa[jj] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (int)(m < nb && c < cols ? off : kOut), 0, 0);
+        xb[jj] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (int)(m < nb && c + 32 < cols ? off + 64 : kOut), 0, 0);
+      }
     }
   };
   int s = wave;
-  if (s < ntiles) {
+  if (kXl || s < ntiles) {
     load_w(s);
   }
   for (; s < ntiles; s += kW) {
@@ -421,13 +458,29 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
       *reinterpret_cast<u32x4 *>(my + (j * kRowsPerInst + lr) * kStride + lc) = cur[j];
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (s + kW < ntiles) {
+    if (kXl || s + kW < ntiles) {
       load_w(s + kW);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kXl) {
+#pragma unroll
+      for (int i = 0; i < kXInst; ++i) {
+        const int n = i * kXRowsPerInst + lane / kXLanesPerRow;
+        *reinterpret_cast<u32x4 *>(myx + n * kXStride + (lane % kXLanesPerRow) * 16) = xl[i];
+      }
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if constexpr (kXl) {
+      /* operand order: batch row m, columns 64 jj + 8 g (and + 32) */
+#pragma unroll
+      for (int jj = 0; jj < kSteps; ++jj) {
+        const int8_t *px = myx + m * kXStride + 128 * jj + 16 * g;
+        xa[jj] = *reinterpret_cast<const u32x4 *>(px);
+        xb[jj] = *reinterpret_cast<const u32x4 *>(px + 64);
+      }
+    }
 #pragma unroll
     for (int jj = 0; jj < kSteps; ++jj) {
 #pragma unroll
@@ -477,6 +530,11 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
 #ifndef VX_GEMV_LDS_COLS
 #define VX_GEMV_LDS_COLS 256
 #endif
+/* x through LDS on 16-row tiles whose grid fits one round, batches of 8
+ * and more (kXl above). */
+#ifndef VX_GEMV_XLDS
+#define VX_GEMV_XLDS 1
+#endif
 
 template <int kR>
 void launch_lds(const int8_t *w, const float *s, const uint16_t *x, float *y,
@@ -484,8 +542,13 @@ void launch_lds(const int8_t *w, const float *s, const uint16_t *x, float *y,
   const int grid = (rows + 16 * kR - 1) / (16 * kR);
   constexpr int kW = kR == 1 ? VX_GEMV_LDS_W : 8;
   constexpr int kCols = kR == 1 ? VX_GEMV_LDS_COLS : 256;
-  hipLaunchKernelGGL((gemv_i8_lds<kW, kCols, kR>), dim3(grid), dim3(kW * 64), 0,
-                     stream, w, s, x, y, rows, cols, nb);
+  if (kR == 1 && VX_GEMV_XLDS && nb >= 8 && grid <= device_cu_count()) {
+    hipLaunchKernelGGL((gemv_i8_lds<kW, kCols, 1, true>), dim3(grid), dim3(kW * 64), 0,
+                       stream, w, s, x, y, rows, cols, nb);
+  } else {
+    hipLaunchKernelGGL((gemv_i8_lds<kW, kCols, kR, false>), dim3(grid), dim3(kW * 64), 0,
+                       stream, w, s, x, y, rows, cols, nb);
+  }
 }
 
 /* Batches of 3 and 4: 8 rows per workgroup, 4 in flight per thread. A

@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
@@ -66,6 +67,23 @@ __host__ __device__ inline uint16_t f32_to_f16(float f) {
 }
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+/* Compute units of the device current at the first call (256 if it cannot
+ * be read); launch shapes are sized by it. */
+inline int device_cu_count() {
+  static std::atomic<int> cached{0};
+  int n = cached.load();
+  if (n == 0) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    n = hipGetDevice(&dev) == hipSuccess &&
+                hipGetDeviceProperties(&prop, dev) == hipSuccess
+            ? prop.multiProcessorCount
+            : 256;
+    cached.store(n);
+  }
+  return n;
+}
 
 } // namespace vxk
 
