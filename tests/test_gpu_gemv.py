@@ -83,6 +83,9 @@ KERNEL_CASES = [
     # a partial last tile and batch rows past nb
     (abi.GEMV_LDS, (4096, 1040), 8), (abi.GEMV_LDS, (4099, 1040), 8),
     (abi.GEMV_LDS, (100, 2064), 9),
+    # batches of 8 and more over 8192 rows: 48-row tiles (171 workgroups), and
+    # 64-row tiles where 48-row ones would not fit one round (258 > 256 CUs)
+    (abi.GEMV_LDS, (8200, 1040), 16), (abi.GEMV_LDS, (12340, 272), 8),
 ]
 
 

@@ -599,7 +599,7 @@ std::atomic<int> forced_gemv{0};
  * with the batch but overlaps the stream, for batches 3 and 4 over at most
  * 4096 columns; otherwise the MFMA kernel, whose cost beyond the weight
  * stream is the x operand, read once per 16 (or, for batches of 8 and more
- * over 8192 rows and more, 64) rows. */
+ * over 8192 rows and more, 48 or 64) rows. */
 GemvKernel gemv_pick(int rows, int cols, int nb) {
   (void)rows;
   if (nb == 1 || (nb == 2 && cols <= kGroupCols)) {
@@ -653,7 +653,13 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
     break;
   case GEMV_LDS:
     if (nb >= 8 && r >= 8192) {
-      launch_lds<4>(w, scale, x, y, r, c, nb, stream);
+      /* 48-row tiles while their grid fits one round (one workgroup per CU
+       * at 104 KiB of LDS), else 64 */
+      if ((r + 47) / 48 <= device_cu_count()) {
+        launch_lds<3>(w, scale, x, y, r, c, nb, stream);
+      } else {
+        launch_lds<4>(w, scale, x, y, r, c, nb, stream);
+      }
     } else {
       launch_lds<1>(w, scale, x, y, r, c, nb, stream);
     }
