@@ -56,7 +56,8 @@ def test_llama7b_shapes(hiplib, shape, batch):
                                          ((8200, 1040), 12), ((17, 4112), 1), ((100, 48), 6),
                                          ((8195, 4096), 16), ((31, 4160), 4),
                                          ((4099, 4096), 2), ((6, 4096), 3), ((5, 8208), 1),
-                                         ((13, 12304), 1), ((3, 20480), 1), ((7, 2064), 4)])
+                                         ((13, 12304), 1), ((3, 20480), 1), ((7, 2064), 4),
+                                         ((8197, 272), 3), ((8197, 4112), 6)])
 def test_ragged(hiplib, shape, batch, rng):
     """Rows that leave the last 16- or 32-row block (or 4-row group) partial,
     columns that end inside a 256-column tile, a 64-column step or a

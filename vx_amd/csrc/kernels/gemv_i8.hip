@@ -353,11 +353,11 @@ __device__ __forceinline__ f32x4 mfma_bf16(const uint32_t *a, u32x4 b, f32x4 c) 
  * tile past the last has every column past `cols`), so the multiply waits
  * for x alone (behind a branch the compiler's waits at the join count the
  * prefetch as possibly absent, and each tile's last MFMA waited for it).
- * The x tile makes a workgroup's LDS 100 KiB, one workgroup per CU, so the
- * launch takes it only when the grid fits one round, and for batches of 8
- * and more (below, most of the tile is zeros and its LDS round trip cost
- * more than the whole lines saved). The branch-free prefetch alone, or on
- * 64-row tiles, measured slower.
+ * The launch takes it with 128-column tiles (measured faster than 256 with
+ * the x tile) when the grid fits one round, for batches of 8 and more
+ * (below, most of the tile is zeros and its LDS round trip cost more than
+ * the whole lines saved). The branch-free prefetch alone, or on 64-row
+ * tiles without the x tile, measured slower.
  *
  * Workgroup g owns rows 16 kR g ..; its kW waves take the column tiles w,
  * w + kW, ...; their accumulators meet in LDS at the end. */
@@ -375,7 +375,6 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
   constexpr uint32_t kOut = 0x80000000u; /* past every range */
   /* x tile (kXl): 16 batch rows of kCols bf16, rows padded by 16 bytes;
    * each load instruction covers 64 * 16 bytes of it in whole lines. */
-  static_assert(!kXl || kR == 1, "x tiles are built for 16-row tiles");
   constexpr int kXStride = kCols * 2 + 16;
   constexpr int kXLanesPerRow = kCols * 2 / 16;
   constexpr int kXRowsPerInst = 64 / kXLanesPerRow;
@@ -530,8 +529,8 @@ __global__ __launch_bounds__(kW * 64) void gemv_i8_lds(
 #ifndef VX_GEMV_LDS_COLS
 #define VX_GEMV_LDS_COLS 256
 #endif
-/* x through LDS on 16-row tiles whose grid fits one round, batches of 8
- * and more (kXl above). */
+/* x through LDS (kXl above): batches of 8 and more on 16-row tiles whose
+ * grid fits one round, and the 48-row tiles. */
 #ifndef VX_GEMV_XLDS
 #define VX_GEMV_XLDS 1
 #endif
@@ -542,8 +541,14 @@ void launch_lds(const int8_t *w, const float *s, const uint16_t *x, float *y,
   const int grid = (rows + 16 * kR - 1) / (16 * kR);
   constexpr int kW = kR == 1 ? VX_GEMV_LDS_W : 8;
   constexpr int kCols = kR == 1 ? VX_GEMV_LDS_COLS : 256;
-  if (kR == 1 && VX_GEMV_XLDS && nb >= 8 && grid <= device_cu_count()) {
-    hipLaunchKernelGGL((gemv_i8_lds<kW, kCols, 1, true>), dim3(grid), dim3(kW * 64), 0,
+  /* x through LDS, 128-column tiles: 16-row tiles (53 KiB of LDS) for
+   * batches of 8 and more when the grid fits one round of the CUs; 48-row
+   * tiles (88 KiB; the caller sends them only grids of one round) */
+  if (VX_GEMV_XLDS && kR == 3) {
+    hipLaunchKernelGGL((gemv_i8_lds<8, 128, 3, true>), dim3(grid), dim3(8 * 64), 0,
+                       stream, w, s, x, y, rows, cols, nb);
+  } else if (VX_GEMV_XLDS && kR == 1 && nb >= 8 && grid <= device_cu_count()) {
+    hipLaunchKernelGGL((gemv_i8_lds<kW, 128, 1, true>), dim3(grid), dim3(kW * 64), 0,
                        stream, w, s, x, y, rows, cols, nb);
   } else {
     hipLaunchKernelGGL((gemv_i8_lds<kW, kCols, kR, false>), dim3(grid), dim3(kW * 64), 0,
@@ -592,20 +597,27 @@ void launch_rows(const int8_t *w, const float *s, const uint16_t *x, float *y,
 
 std::atomic<int> forced_gemv{0};
 
+/* Batches of 3 and more over 8192 rows and more go to 48-row MFMA tiles
+ * with x through LDS while their grid fits one round of the CUs. */
+bool tall_tiles(int rows, int nb) {
+  return VX_GEMV_XLDS && nb >= 3 && rows >= 8192 && (rows + 47) / 48 <= device_cu_count();
+}
+
 /* The automatic choice, from sweeps of every kernel over 4096 x 4096,
  * 11008 x 4096 and 4096 x 11008: gemv_i8_rows (dot2; each workgroup one
  * burst of loads) for batch 1 at any width and batch 2 over at most 4096
  * columns; the grid-stride dot2 kernel, whose work per weight byte grows
  * with the batch but overlaps the stream, for batches 3 and 4 over at most
- * 4096 columns; otherwise the MFMA kernel, whose cost beyond the weight
- * stream is the x operand, read once per 16 (or, for batches of 8 and more
- * over 8192 rows and more, 48 or 64) rows. */
+ * 4096 columns, except over 8192 rows and more, where 48-row MFMA tiles
+ * with x through LDS take batches from 3 while their grid fits one round;
+ * otherwise the MFMA kernel, whose cost beyond the weight stream is the x
+ * operand, read once per 16 (or 48, or for batches of 8 and more over 8192
+ * rows and more 64) rows. */
 GemvKernel gemv_pick(int rows, int cols, int nb) {
-  (void)rows;
   if (nb == 1 || (nb == 2 && cols <= kGroupCols)) {
     return GEMV_ROWS;
   }
-  if (nb <= 4 && cols <= kGroupCols) {
+  if (nb <= 4 && cols <= kGroupCols && !tall_tiles(rows, nb)) {
     return GEMV_DOT2_B4;
   }
   return GEMV_LDS;
@@ -652,14 +664,11 @@ bool gemv_i8_launch(const int8_t *w, const float *scale, const uint16_t *x,
     launch_b4(w, scale, x, y, r, c, nb, stream);
     break;
   case GEMV_LDS:
-    if (nb >= 8 && r >= 8192) {
-      /* 48-row tiles while their grid fits one round (one workgroup per CU
-       * at 104 KiB of LDS), else 64 */
-      if ((r + 47) / 48 <= device_cu_count()) {
-        launch_lds<3>(w, scale, x, y, r, c, nb, stream);
-      } else {
-        launch_lds<4>(w, scale, x, y, r, c, nb, stream);
-      }
+    if (tall_tiles(r, nb)) {
+      /* 48-row tiles, one round (one workgroup per CU) */
+      launch_lds<3>(w, scale, x, y, r, c, nb, stream);
+    } else if (nb >= 8 && r >= 8192) {
+      launch_lds<4>(w, scale, x, y, r, c, nb, stream);
     } else {
       launch_lds<1>(w, scale, x, y, r, c, nb, stream);
     }
