@@ -9,8 +9,9 @@
  * MFMA through the transposing ds_read_b64_tr_b16; the two waves that share
  * a SIMD alternate between loading operands and computing, so the MFMA pipe,
  * the LDS and the load path work at the same time. Workgroups are renumbered
- * so the 32 consecutive tiles each XCD receives form a 4x8 patch of C, which
- * keeps each XCD's A and B panels in its own L2.
+ * so the 32 consecutive tiles each XCD receives form a patch of C (4 tile
+ * rows deep; 2 for a grid of at most one round), which keeps each XCD's A
+ * and B panels in its own L2.
  *
  * gemm_tiled takes every supported type pair, any shape and row stride:
  * 64x64 tiles, 16-deep K stages through LDS, one multiply and one add per
@@ -42,7 +43,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileM = 256;
 constexpr int kTileN = 256;
-constexpr int kGroupM = 4; /* tile rows per launch-order group */
+/* Tile rows per launch-order group: 4, and 2 for grids of at most one
+ * round (256 tiles). Measured on the ping-pong kernel (bf16 -> f32, paired
+ * runs on one box): 4096^3 with groups of 1, 2, 4 and 16 rows 1231-1235,
+ * 1231-1235, 1196-1201 and 1220-1230 TFLOP/s; 8192^3 with 2, 4, 8 and 16
+ * rows 1240-1254, 1282-1290, 1269-1280 and 1248-1255. */
+constexpr int kGroupM = 4;
+constexpr int kSmallGrid = 256;
+constexpr int kSmallGroupM = 2;
 
 template <int kOut>
 __device__ __forceinline__ void put(void *c, int64_t at, float v) {
@@ -232,9 +240,10 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
   if ((nwg & 7) == 0) {
     id = (id & 7) * (nwg >> 3) + (id >> 3);
   }
-  const int group_size = kGroupM * tiles_n;
-  const int first_m = (id / group_size) * kGroupM;
-  const int rows_in_group = min(tiles_m - first_m, kGroupM);
+  const int group_m = tiles_m * tiles_n <= kSmallGrid ? kSmallGroupM : kGroupM;
+  const int group_size = group_m * tiles_n;
+  const int first_m = (id / group_size) * group_m;
+  const int rows_in_group = min(tiles_m - first_m, group_m);
   const int in_group = id % group_size;
   const int tm = first_m + in_group % rows_in_group;
   const int tn = in_group / rows_in_group;
