@@ -53,10 +53,12 @@ enum {
  * example 512 queries of 32 heads over a long cache) may cut the key range
  * into splits and merge them in f32 (same result to within f32 rounding
  * before the one bf16 rounding). The split partials live in HBM the
- * library keeps per (device, stream) for the rest of the process: at most
- * 8 x batch x heads x seq_q x (head_dim + 1) x 4 bytes, taken in the
- * stream's order. A stream that is capturing a graph gets the unsplit
- * launch. */
+ * library keeps per (device, stream): at most 8 x batch x heads x seq_q x
+ * (head_dim + 1) x 4 bytes, taken in the stream's order. A stream's block
+ * is freed, in its order, when the calling thread's stream is set to
+ * another one (so set another stream, or NULL, before destroying one); the
+ * default stream's block stays until the process ends. A stream that is
+ * capturing a graph gets the unsplit launch. */
 int32_t vx_nn_flash_attention_fwd_bf16(const uint16_t *q, const uint16_t *k,
                                        const uint16_t *v, uint16_t *o,
                                        float *lse, int64_t batch, int64_t heads,
@@ -201,8 +203,11 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
  * object) instead of the staging pool. Returns 1 when the GEMM was issued,
  * 0 (reason on stderr, nothing launched) for a region that is not a routed
  * GEMM, a result published through a slot (host memory the program frees),
- * or staging beyond 16 MiB. Operands already in GPU memory need no staging.
- * Calls on one GPU share its array: calls that overlap in time race. */
+ * staging beyond 16 MiB, or staging while the caller stream is capturing a
+ * graph. Operands already in GPU memory need no staging. Calls on one GPU
+ * share its array and take turns on it: a call that stages waits, in its
+ * stream's order, for the GEMM of the previous such call (on any stream or
+ * thread) before it overwrites the array. */
 uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
                                        size_t payload_size, void **device_args,
                                        const int32_t *arg_tags,

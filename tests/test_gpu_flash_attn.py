@@ -1,6 +1,8 @@
 """The flash-attention forward op on the GPU against the CPU oracle (f64
 two-pass softmax), including the full BASELINE config on sampled rows."""
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -14,14 +16,23 @@ from vx_amd.runtime import DeviceArray, HipTimer, flash_attention_fwd
 pytestmark = pytest.mark.gpu
 
 
-def run(lib, q16, k16, v16, heads, kv_heads, scale, causal, with_lse=True):
+BF16_NAN = 0x7FC0
+
+
+def run(lib, q16, k16, v16, heads, kv_heads, scale, causal, with_lse=True, poison=False):
+    """One launch. With `poison` the output and lse buffers start as NaN, so
+    an element the kernel never writes stays NaN."""
     b, _, sq, d = q16.shape
     sk = k16.shape[2]
     dq = DeviceArray.of(lib, q16, abi.DTYPE_BF16)
     dk = DeviceArray.of(lib, k16, abi.DTYPE_BF16)
     dv = DeviceArray.of(lib, v16, abi.DTYPE_BF16)
-    do = DeviceArray(lib, q16.shape, abi.DTYPE_BF16)
-    dl = DeviceArray(lib, (b, heads, sq), abi.DTYPE_F32) if with_lse else None
+    if poison:
+        do = DeviceArray.of(lib, np.full(q16.shape, BF16_NAN, np.uint16), abi.DTYPE_BF16)
+        dl = DeviceArray.of(lib, np.full((b, heads, sq), np.nan, np.float32), abi.DTYPE_F32)
+    else:
+        do = DeviceArray(lib, q16.shape, abi.DTYPE_BF16)
+        dl = DeviceArray(lib, (b, heads, sq), abi.DTYPE_F32) if with_lse else None
     rc = flash_attention_fwd(lib, dq.ptr, dk.ptr, dv.ptr, do.ptr, dl.ptr if dl else None, b, heads,
                              kv_heads, sq, sk, d, scale, causal)
     assert rc == 0
@@ -80,23 +91,55 @@ def test_closed_forms(hiplib, rng):
     assert_max_abs(l0, np.broadcast_to(np.log(np.arange(1, s + 1)), l0.shape), 1e-4, "ln count")
 
 
+def numpy_head_f64(q16, k16, v16, bi, hi, scale):
+    """Causal softmax(q k^T * scale) v of one whole head in f64, vectorised
+    (written independently of the C oracle)."""
+    q = bf16_to_f32(q16[bi, hi]).astype(np.float64)
+    k = bf16_to_f32(k16[bi, hi]).astype(np.float64)
+    v = bf16_to_f32(v16[bi, hi]).astype(np.float64)
+    s = (q @ k.T) * scale
+    s[np.triu_indices(s.shape[0], 1)] = -np.inf
+    m = s.max(axis=1, keepdims=True)
+    p = np.exp(s - m)
+    l = p.sum(axis=1, keepdims=True)
+    return (p @ v) / l, (m + np.log(l))[:, 0]
+
+
 def test_baseline_config_sampled(hiplib):
     """[4, 32, 2048, 128] causal, N(0,1), scale 1/sqrt(128).
-    Rows sampled across batches, heads and block boundaries."""
+
+    The output and lse start as NaN, so every element being finite proves the
+    launch wrote all of them. Against the f64 oracle: the first and last row
+    of every (batch, head), one row in every 128-query block of every head
+    (the unit the launch order maps workgroups to, at a different offset per
+    block), and extra rows at block boundaries; one whole head per batch is
+    compared row by row against a numpy f64 softmax. A launch order that ran
+    one (head, block) twice and skipped another fails here."""
     announce("flash attn config 3")
     rng = np.random.default_rng(7)
     b, h, s, d = 4, 32, 2048, 128
     q16, k16, v16 = (randn16(rng, (b, h, s, d)) for _ in range(3))
     scale = 1.0 / np.sqrt(d)
-    o, lse = run(hiplib, q16, k16, v16, h, h, scale, True)
-    picks = [0, 1, 31, 32, 63, 64, 127, 128, 129, 1000, 1023, 1024, 2046, 2047]
-    rows = np.array([(bi, hi, qi) for bi in range(b) for hi in (0, 13, 31) for qi in picks],
-                    np.int64)
+    o, lse = run(hiplib, q16, k16, v16, h, h, scale, True, poison=True)
+    assert np.isfinite(o).all() and np.isfinite(lse).all(), "unwritten output or lse"
+    rows = set()
+    for bi in range(b):
+        for hi in range(h):
+            rows.update({(bi, hi, 0), (bi, hi, s - 1)})
+            for qb in range(s // 128):
+                rows.add((bi, hi, qb * 128 + ((bi * h + hi) * 37 + qb * 11) % 128))
+    picks = [1, 31, 32, 63, 64, 127, 128, 129, 1000, 1023, 1024, 2046]
+    rows.update((bi, hi, qi) for bi in range(b) for hi in (0, 13, 31) for qi in picks)
+    rows = np.array(sorted(rows), np.int64)
     wo, wl = oracle.attention_rows(q16, k16, v16, h, h, scale, True, rows)
     got = o[rows[:, 0], rows[:, 1], rows[:, 2]]
     assert_max_abs(got, wo, BF16_ABS, "config 3 rows")
     assert_max_abs(lse[rows[:, 0], rows[:, 1], rows[:, 2]], wl, 1e-3, "config 3 lse")
-    assert np.isfinite(o).all()
+    for bi in range(b):
+        hi = (11 * bi + 5) % h
+        wo_head, wl_head = numpy_head_f64(q16, k16, v16, bi, hi, scale)
+        assert_max_abs(o[bi, hi], wo_head, BF16_ABS, f"config 3 whole head ({bi}, {hi})")
+        assert_max_abs(lse[bi, hi], wl_head, 1e-3, f"config 3 whole head lse ({bi}, {hi})")
 
 
 @pytest.mark.parametrize("start", [0, 1536, 7680])
@@ -282,6 +325,56 @@ def test_split_workspaces_from_threads(hiplib):
         th.join(timeout=90)
     assert not any(th.is_alive() for th in threads), "a launching thread did not finish"
     assert not errors, errors
+
+
+def fa_workspaces(lib):
+    out = (ctypes.c_int64 * 2)()
+    assert lib.control(abi.HIP_CTRL_FA_WORKSPACES, out) == 1
+    return out[0], out[1]
+
+
+def test_split_workspace_freed_with_stream(hiplib, rng):
+    """Streams created and destroyed in a loop, each splitting a launch:
+    setting the thread's stream back to NULL frees that stream's workspace
+    (so none is left for a destroyed stream, and a new stream at a reused
+    address starts with none), and every loop's result is the same."""
+    announce("flash attn split workspace per stream lifetime")
+    b, h, hk, sq, sk, d = 1, 4, 2, 64, 1024, 128
+    q16, k16, v16 = randn16(rng, (b, h, sq, d)), randn16(rng, (b, hk, sk, d)), randn16(rng, (b, hk, sk, d))
+    scale = 1.0 / np.sqrt(d)
+    dq, dk, dv = (DeviceArray.of(hiplib, x, abi.DTYPE_BF16) for x in (q16, k16, v16))
+    do = DeviceArray(hiplib, (b, h, sq, d), abi.DTYPE_BF16)
+    dl = DeviceArray(hiplib, (b, h, sq), abi.DTYPE_F32)
+    t = HipTimer()
+    first = None
+    try:
+        hiplib.force_fa_splits(4)
+        base_blocks, _ = fa_workspaces(hiplib)
+        for it in range(6):
+            s = t.stream_create()
+            try:
+                hiplib.lib.vx_hip_set_stream(s)
+                assert flash_attention_fwd(hiplib, dq.ptr, dk.ptr, dv.ptr, do.ptr, dl.ptr, b, h, hk,
+                                           sq, sk, d, scale, True) == 0
+                blocks, nbytes = fa_workspaces(hiplib)
+                assert blocks == base_blocks + 1 and nbytes >= 4 * b * h * sq * (d + 1) * 4, it
+                got = (do.numpy().copy(), dl.numpy().copy())
+            finally:
+                hiplib.lib.vx_hip_set_stream(None)
+                t.sync()
+                t.stream_destroy(s)
+            assert fa_workspaces(hiplib)[0] == base_blocks, f"loop {it}: workspace kept"
+            if first is None:
+                first = got
+            assert np.array_equal(got[0], first[0]) and np.array_equal(got[1], first[1]), it
+        wo, wl = oracle.attention_rows(q16, k16, v16, h, hk, scale, True,
+                                       oracle.attention_all_rows(b, h, sq))
+        assert_max_abs(bf16_to_f32(first[0]).reshape(-1, d), wo, BF16_ABS, "split per stream")
+    finally:
+        hiplib.force_fa_splits(0)
+        hiplib.lib.vx_hip_set_stream(None)
+        for x in (dq, dk, dv, do, dl):
+            x.free()
 
 
 def test_split_control_refusals(hiplib):

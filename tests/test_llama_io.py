@@ -157,3 +157,96 @@ def test_step_byte_counts(cfg):
         rows_read = pos + 1
         per_layer = 2 * (rows_read + 1) * cfg.kv_dim * np.dtype(np.float32).itemsize
         assert cfg.kv_bytes(pos) == cfg.n_layers * per_layer
+
+
+# ---- the RoPE table against the reference's correctly rounded f32 maths ----
+
+_DIGITS = 60
+
+
+def _dec_pi():
+    from decimal import Decimal
+    return Decimal("3.14159265358979323846264338327950288419716939937510582097494459230781640628620899")
+
+
+def _dec_cos_sin(x: float):
+    """cos and sin of a double to about 55 digits: reduction by a 80-digit
+    pi, then the Taylor series."""
+    from decimal import Decimal, localcontext
+    with localcontext() as ctx:
+        ctx.prec = _DIGITS
+        x = Decimal(x)
+        two_pi = 2 * _dec_pi()
+        r = x - (x / two_pi).to_integral_value() * two_pi
+        eps = Decimal(10) ** -(_DIGITS - 5)
+        out = []
+        for first, start in ((Decimal(1), 0), (r, 1)):
+            t, acc, i = first, Decimal(0), start
+            while abs(t) > eps:
+                acc += t
+                i += 2
+                t = -t * r * r / (i * (i - 1))
+            out.append(acc)
+        return out[0], out[1]
+
+
+def _dec_pow10000(e: float):
+    from decimal import Decimal, localcontext
+    with localcontext() as ctx:
+        ctx.prec = _DIGITS
+        return (Decimal(e) * Decimal(10000).ln()).exp()
+
+
+def _round_f32(d) -> np.float32:
+    """The f32 nearest to the Decimal d (ties cannot occur at these digits)."""
+    from decimal import Decimal
+    f = np.float32(float(d))
+    cands = [f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))]
+    return min(cands, key=lambda g: abs(Decimal(float(g)) - d))
+
+
+def _near_midpoint(v: float, ulps: float = 64.0) -> bool:
+    """Whether the double v lies within `ulps` double ulps of a point halfway
+    between two f32 values (where a double evaluation off by under one ulp
+    could round to the other f32)."""
+    f = np.float32(v)
+    up = np.nextafter(f, np.float32(np.inf)) if float(f) <= v else f
+    lo = f if float(f) <= v else np.nextafter(f, np.float32(-np.inf))
+    mid = (float(lo) + float(up)) / 2.0
+    return abs(v - mid) <= ulps * abs(np.spacing(v))
+
+
+@pytest.mark.parametrize("hs,positions", [(64, 1024), (128, 512), (16, 256)])
+def test_rope_table_is_correctly_rounded(hs, positions):
+    """Reference examples/llama.vx:244-246 takes f32 cos and sin of the f32
+    angle pos * 10000^(-i/hs), with powf, cos and sin documented as correctly
+    rounded (reference stdlib/core/num.vx:2434-2442, 2476-2479). Every
+    inverse frequency is checked against a 60-digit power. Each table entry
+    whose double evaluation lies near an f32 rounding midpoint (where a
+    rounding of the double could differ from the correct one) is checked
+    against a 60-digit cos/sin, and so are 200 entries picked at random; the
+    others round correctly because glibc's double cos and sin are within one
+    ulp. Config 4's table is the first case."""
+    import math
+
+    cfg = llama.LlamaConfig(dim=hs * 4, hidden_dim=64, n_layers=1, n_heads=4, n_kv_heads=4,
+                            vocab_size=32, seq_len=positions)
+    inv = llama.rope_inv_freq(hs)
+    for j, i in enumerate(range(0, hs, 2)):
+        e = float(-np.float32(i) / np.float32(hs))
+        assert inv[j] == _round_f32(_dec_pow10000(e)), (hs, i)
+    tab = llama.rope_table(cfg)
+    assert tab.shape == (positions, hs // 2, 2)
+    ang = (np.arange(positions, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    rng = np.random.default_rng(hs)
+    sample = set(zip(rng.integers(0, positions, 200).tolist(), rng.integers(0, hs // 2, 200).tolist()))
+    checked = 0
+    for p in range(positions):
+        for j in range(hs // 2):
+            a = float(ang[p, j])
+            if (p, j) in sample or _near_midpoint(math.cos(a)) or _near_midpoint(math.sin(a)):
+                c, s = _dec_cos_sin(a)
+                assert tab[p, j, 0] == _round_f32(c), (p, j, "cos")
+                assert tab[p, j, 1] == _round_f32(s), (p, j, "sin")
+                checked += 1
+    assert checked >= len(sample)

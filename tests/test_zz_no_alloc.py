@@ -35,11 +35,22 @@ def noalloc(lib, payload, args) -> int:
     return lib.lib.vx_hip_dispatch_async_noalloc(buf, len(payload), argv, tags, n)
 
 
+def staging(lib):
+    """(staging-pool acquires, of them new allocations, bytes staged through
+    the no-alloc scratch)."""
+    out = (ctypes.c_int64 * 3)()
+    assert lib.control(abi.HIP_CTRL_STAGING_STATS, out) == 1
+    return tuple(out)
+
+
 def via_both(lib, a, b, a_dt, out_dt, host_out=True):
     """C through the ABI entry point and through the no-alloc one, from
-    host operands (and a host or device result)."""
+    host operands (and a host or device result). The ABI entry point stages
+    through its pool; the no-alloc one takes nothing from the pool and
+    stages every host byte through its scratch."""
     m, n = a.shape[0], b.shape[1]
     np_out = np.float32 if out_dt == abi.DTYPE_F32 else np.uint16
+    staged = a.nbytes + b.nbytes + (m * n * np.dtype(np_out).itemsize if host_out else 0)
     results = []
     for entry in ("abi", "noalloc"):
         if host_out:
@@ -48,10 +59,16 @@ def via_both(lib, a, b, a_dt, out_dt, host_out=True):
             c = DeviceArray(lib, (m, n), out_dt)
         args = gemm_args(a, a_dt, b, a_dt, c, out_dt)
         before = lib.stats()
+        pool0 = staging(lib)
         if entry == "abi":
             lib.dispatch(abi.matmul_payload(), args)
+            pool1 = staging(lib)
+            assert pool1[0] == pool0[0] + (3 if host_out else 2) and pool1[2] == pool0[2]
         else:
             assert noalloc(lib, abi.matmul_payload(), args) == 1
+            pool1 = staging(lib)
+            assert pool1[:2] == pool0[:2], "the no-alloc entry point used the pool"
+            assert pool1[2] == pool0[2] + staged
         st = lib.stats()
         assert st["gemm_device"] == before["gemm_device"] + 1
         if host_out:
@@ -114,3 +131,40 @@ def test_noalloc_resident_operands_and_refusals(hiplib, rng):
     assert np.all(big_c == 7)
     for x in (da, db, dc1, dc2):
         x.free()
+
+
+def test_noalloc_calls_on_two_streams_take_turns(hiplib, rng):
+    """Two calls with host operands on two streams, the second issued while
+    the first one's GEMM may still read the scratch: the second call's
+    stream waits for it, so both results match the oracle."""
+    import oracle
+    from vx_amd.runtime import HipTimer
+
+    announce("noalloc GEMM: two streams, host bf16 operands 512x2048x1024 each")
+    t = HipTimer()
+    streams = [t.stream_create(), t.stream_create()]
+    cases, outs = [], []
+    try:
+        for i, s in enumerate(streams):
+            a16 = f32_to_bf16(rng.normal(0, 1 / 32, (512, 2048)).astype(np.float32))
+            b16 = f32_to_bf16(rng.normal(0, 1 / 32, (2048, 1024)).astype(np.float32))
+            c = DeviceArray(hiplib, (512, 1024), abi.DTYPE_F32)
+            cases.append((a16, b16))
+            outs.append(c)
+            hiplib.lib.vx_hip_set_stream(s)
+            assert noalloc(hiplib, abi.matmul_payload(),
+                           gemm_args(a16, abi.DTYPE_BF16, b16, abi.DTYPE_BF16, c,
+                                     abi.DTYPE_F32)) == 1
+        hiplib.lib.vx_hip_set_stream(None)
+        t.sync()
+        for (a16, b16), c in zip(cases, outs):
+            want = oracle.gemm_bf16_f32(a16, b16)
+            got = c.numpy()
+            assert np.abs(got - want).max() <= 1e-4 * max(1.0, float(np.abs(want).max()))
+    finally:
+        hiplib.lib.vx_hip_set_stream(None)
+        t.sync()
+        for s in streams:
+            t.stream_destroy(s)
+        for c in outs:
+            c.free()

@@ -45,6 +45,8 @@ HIP_CTRL_IMAGE_STATS = CTRL_VENDOR_BASE + 4
 HIP_CTRL_CLOCK_STAMPS = CTRL_VENDOR_BASE + 5
 HIP_CTRL_GEMV_KERNEL = CTRL_VENDOR_BASE + 6
 HIP_CTRL_FA_SPLITS = CTRL_VENDOR_BASE + 7
+HIP_CTRL_FA_WORKSPACES = CTRL_VENDOR_BASE + 8
+HIP_CTRL_STAGING_STATS = CTRL_VENDOR_BASE + 9
 # Kernels the GEMV control opcode can force (0 = automatic choice).
 GEMV_AUTO, GEMV_ROWS, GEMV_DOT2_B4, GEMV_LDS = 0, 1, 2, 3
 # Kernels the GEMM control opcode can force (0 = automatic choice).

@@ -355,6 +355,7 @@ std::atomic<int64_t> stat_gemm_mfma{0};
 std::atomic<int64_t> stat_gemm_tiled{0};
 std::atomic<int64_t> stat_host_fallback{0};
 std::atomic<int64_t> stat_staged_bytes{0};
+std::atomic<int64_t> stat_scratch_staged_bytes{0}; /* of them, via the scratch */
 std::atomic<int64_t> stat_image_launches{0};
 std::atomic<int64_t> stat_image_loads{0};
 std::atomic<int> forced_gemm_kernel{0};
@@ -428,6 +429,9 @@ void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
   out.pooled = arena == nullptr;
   out.row_stride = cols;
   stat_staged_bytes += (int64_t)out.bytes;
+  if (arena) {
+    stat_scratch_staged_bytes += (int64_t)out.bytes;
+  }
   VX_HIP_CHECK(hipMemcpy2DAsync(out.ptr, width, data, (size_t)row_stride * esz,
                                 width, (size_t)rows, hipMemcpyHostToDevice,
                                 caller_stream));
@@ -465,6 +469,9 @@ bool run_gemm(const vx_gemm_plan &plan, Arena *arena = nullptr) {
     }
     c.pooled = arena == nullptr;
     c.row_stride = plan.n;
+    if (arena) {
+      stat_scratch_staged_bytes += (int64_t)c.bytes;
+    }
   }
 
   vxk::GemmArgs g;
@@ -941,21 +948,29 @@ void one_rank_copy(const void *in, void *out, int64_t count, size_t esz,
 constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
+/* One device's scratch: its address and the event recorded after the last
+ * call that staged through it (null until then). */
+struct Scratch {
+  unsigned char *ptr = nullptr;
+  hipEvent_t done = nullptr;
+  std::mutex use; /* held by a call from its first staging copy to its record */
+};
+
 std::mutex scratch_mutex;
-std::map<int, unsigned char *> &scratch_ptrs() {
-  static auto *m = new std::map<int, unsigned char *>();
+std::map<int, Scratch> &scratch_table() {
+  static auto *m = new std::map<int, Scratch>();
   return *m;
 }
 
-/* This device's scratch, looked up once per device with that device
- * current; null (message printed) when the lookup fails. */
-unsigned char *noalloc_scratch() {
+/* This device's scratch, looked up (and its event created) once per device
+ * with that device current; null (message printed) when the lookup fails. */
+Scratch *noalloc_scratch() {
   int device = 0;
   VX_HIP_CHECK(hipGetDevice(&device));
   std::lock_guard<std::mutex> hold(scratch_mutex);
-  auto found = scratch_ptrs().find(device);
-  if (found != scratch_ptrs().end()) {
-    return found->second;
+  Scratch &sc = scratch_table()[device];
+  if (sc.ptr) {
+    return &sc;
   }
   void *ptr = nullptr;
   const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
@@ -967,9 +982,18 @@ unsigned char *noalloc_scratch() {
             device, hipGetErrorString(e));
     return nullptr;
   }
-  unsigned char *p = static_cast<unsigned char *>(ptr);
-  scratch_ptrs()[device] = p;
-  return p;
+  hipEvent_t ev = nullptr;
+  const hipError_t ee = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (ee != hipSuccess) {
+    (void)hipGetLastError();
+    fprintf(stderr,
+            "[Vx HIP] vx_hip_dispatch_async_noalloc: no event on GPU %d: %s\n",
+            device, hipGetErrorString(ee));
+    return nullptr;
+  }
+  sc.ptr = static_cast<unsigned char *>(ptr);
+  sc.done = ev;
+  return &sc;
 }
 
 } // namespace
@@ -1066,12 +1090,16 @@ uint64_t vx_plugin_dispatch_async(const void *binary_payload,
 
 /* The kind=matmul dispatch without allocating: host operands and a host
  * result buffer are staged through this device's fixed scratch instead of
- * the pool. Everything else the ABI entry point would do that allocates is
- * refused (returns 0 with the reason on stderr, nothing launched): regions
- * that are not a routed GEMM, results published through a slot (the
- * program frees those with free()), and staging beyond the scratch. Calls
- * on one GPU share its scratch: calls that overlap in time (other streams,
- * other threads) race. */
+ * the pool. Everything else the ABI entry point would do that allocates or
+ * blocks is refused (returns 0 with the reason on stderr, nothing
+ * launched): regions that are not a routed GEMM, results published through
+ * a slot (the program frees those with free()), staging beyond the scratch,
+ * and staging while the caller stream captures a graph. Calls on one GPU
+ * share its scratch and are ordered on it: a call that stages holds the
+ * scratch from its first copy to the launch of its GEMM, and its stream
+ * first waits (hipStreamWaitEvent) for the event the previous such call
+ * recorded after its GEMM, so a later call on another stream or thread never
+ * overwrites operands a GEMM still reads. */
 uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
                                        size_t payload_size, void **device_args,
                                        const int32_t *arg_tags,
@@ -1119,18 +1147,36 @@ uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
             op, (unsigned long long)need, kNoAllocScratchBytes);
     return 0;
   }
-  Arena arena;
-  if (need) {
-    arena.base = noalloc_scratch();
-    if (!arena.base) {
+  if (!need) {
+    if (!run_gemm(plan, nullptr)) {
+      fprintf(stderr, "[Vx HIP] %s: no GPU kernel takes this GEMM's types\n",
+              op);
       return 0;
     }
-    arena.size = kNoAllocScratchBytes;
+    return 1;
   }
-  if (!run_gemm(plan, need ? &arena : nullptr)) {
+  if (capturing()) {
+    fprintf(stderr,
+            "[Vx HIP] %s: the caller stream is capturing a graph, and this "
+            "GEMM has host operands or a host result, which a graph cannot "
+            "copy in this call's order\n",
+            op);
+    return 0;
+  }
+  Scratch *sc = noalloc_scratch();
+  if (!sc) {
+    return 0;
+  }
+  std::lock_guard<std::mutex> hold(sc->use);
+  VX_HIP_CHECK(hipStreamWaitEvent(caller_stream, sc->done, 0));
+  Arena arena;
+  arena.base = sc->ptr;
+  arena.size = kNoAllocScratchBytes;
+  if (!run_gemm(plan, &arena)) {
     fprintf(stderr, "[Vx HIP] %s: no GPU kernel takes this GEMM's types\n", op);
     return 0;
   }
+  VX_HIP_CHECK(hipEventRecord(sc->done, caller_stream));
   return 1;
 }
 
@@ -1283,6 +1329,8 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
 #define VX_HIP_CTRL_CLOCK_STAMPS (VX_CTRL_VENDOR_BASE + 5)
 #define VX_HIP_CTRL_GEMV_KERNEL (VX_CTRL_VENDOR_BASE + 6)
 #define VX_HIP_CTRL_FA_SPLITS (VX_CTRL_VENDOR_BASE + 7)
+#define VX_HIP_CTRL_FA_WORKSPACES (VX_CTRL_VENDOR_BASE + 8)
+#define VX_HIP_CTRL_STAGING_STATS (VX_CTRL_VENDOR_BASE + 9)
 
 int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   switch (opcode) {
@@ -1415,6 +1463,29 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     vxk::flash_attn_force_splits(*splits);
     return 1;
   }
+  case VX_HIP_CTRL_STAGING_STATS: {
+    /* payload -> int64_t[3]: staging-pool acquires (reuses plus new
+     * allocations), of them new allocations, bytes staged through the
+     * no-alloc scratch. */
+    int64_t *out = static_cast<int64_t *>(payload);
+    if (!out) {
+      return 0;
+    }
+    out[0] = (int64_t)(pool().hits() + pool().misses());
+    out[1] = (int64_t)pool().misses();
+    out[2] = stat_scratch_staged_bytes.load();
+    return 1;
+  }
+  case VX_HIP_CTRL_FA_WORKSPACES: {
+    /* payload -> int64_t[2]: flash-attention split workspaces held (one per
+     * device and stream that split a launch) and their bytes. */
+    int64_t *out = static_cast<int64_t *>(payload);
+    if (!out) {
+      return 0;
+    }
+    vxk::flash_attn_workspace_stats(&out[0], &out[1]);
+    return 1;
+  }
   case VX_HIP_CTRL_POOL_DRAIN:
     if (hip_available()) {
       wait_for_kernels("pool drain");
@@ -1441,14 +1512,20 @@ int64_t vx_plugin_tensor_map(int64_t base, int64_t rank, int64_t elem_bytes,
 
 /* The caller stream, as a hipStream_t. The CUDA-named pair is what compiled
  * programs and host code already call (reference
- * runtime/cuda_dispatch.cpp:2030-2035); the HIP-named pair is the same. */
-void vx_cuda_set_stream(void *stream) {
-  caller_stream = static_cast<hipStream_t>(stream);
-}
-void *vx_cuda_get_stream(void) { return caller_stream; }
+ * runtime/cuda_dispatch.cpp:2030-2035); the HIP-named pair is the same.
+ * Moving off a stream frees, in that stream's order, the flash-attention
+ * split workspace the library kept for it, so a stream the caller then
+ * destroys leaves nothing behind and a later stream at the same address
+ * starts with none. A stream must stay alive while it is set. */
 void vx_hip_set_stream(void *stream) {
-  caller_stream = static_cast<hipStream_t>(stream);
+  const hipStream_t next = static_cast<hipStream_t>(stream);
+  if (caller_stream && caller_stream != next) {
+    vxk::flash_attn_release_stream(caller_stream);
+  }
+  caller_stream = next;
 }
+void vx_cuda_set_stream(void *stream) { vx_hip_set_stream(stream); }
+void *vx_cuda_get_stream(void) { return caller_stream; }
 void *vx_hip_get_stream(void) { return caller_stream; }
 
 void vx_collective_init(int32_t rank, int32_t ranks) {

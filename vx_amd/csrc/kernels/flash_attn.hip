@@ -731,7 +731,9 @@ int pick_splits(int64_t items, int64_t key_blocks, int cus) {
 
 /* Split partials of one (device, stream). Launches on one stream run in
  * order, so they share the block; it grows (the old block freed in the
- * stream's order) and lives until the process ends. */
+ * stream's order). A stream's block is freed, in that stream's order, when
+ * the caller stream of a thread moves off it (flash_attn_release_stream);
+ * the default stream's block lives until the process ends. */
 struct SplitSpace {
   float *base = nullptr;
   size_t bytes = 0;
@@ -764,6 +766,50 @@ bool reserve(SplitSpace &sp, size_t bytes, hipStream_t stream) {
 } // namespace
 
 void flash_attn_force_splits(int splits) { forced_splits.store(splits > 0 ? splits : 0); }
+
+int flash_attn_release_stream(hipStream_t stream) {
+  if (!stream) {
+    return 0;
+  }
+  /* A stream that is capturing would record the free into its graph: its
+   * block stays until a later release finds it idle. */
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (status != hipStreamCaptureStatusNone) {
+    return 0;
+  }
+  std::lock_guard<std::mutex> hold(spaces_mutex);
+  int freed = 0;
+  auto &m = spaces();
+  for (auto it = m.begin(); it != m.end();) {
+    if (it->first.second != stream) {
+      ++it;
+      continue;
+    }
+    if (it->second.base) {
+      VX_HIP_CHECK(hipFreeAsync(it->second.base, stream));
+      ++freed;
+    }
+    it = m.erase(it);
+  }
+  return freed;
+}
+
+void flash_attn_workspace_stats(int64_t *blocks, int64_t *bytes) {
+  std::lock_guard<std::mutex> hold(spaces_mutex);
+  int64_t n = 0, total = 0;
+  for (const auto &e : spaces()) {
+    if (e.second.base) {
+      ++n;
+      total += (int64_t)e.second.bytes;
+    }
+  }
+  *blocks = n;
+  *bytes = total;
+}
 
 bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
                            const uint16_t *v, uint16_t *o, float *lse,

@@ -91,15 +91,19 @@ void quantize_rows(const float *w, int64_t rows, int64_t cols, int8_t *q,
   }
 }
 
-/* [seq_len, hs / 2, 2] of (cos, sin) of pos * 10000^(-i / hs), even i; the
- * angle in f32 as the reference's RoPE computes it, cos and sin in double
- * then rounded. */
+/* [seq_len, hs / 2, 2] of (cos, sin) of the f32 angle (pos as f32) *
+ * 10000^(-(i as f32) / (hs as f32)), even i, as reference
+ * tests/modules/llama_rt.vx:82-85 and examples/llama.vx:244-246 compute it
+ * with f32 powf, cos and sin, which reference stdlib/core/num.vx:2434-2479
+ * documents as correctly rounded. Each is evaluated in double (glibc, under
+ * 1 ulp of double) and rounded to f32 once. */
 void rope_table(const vx_llama_i8_config &c, std::vector<float> &out) {
   const int hs = c.dim / c.n_heads;
   out.resize((size_t)c.seq_len * (hs / 2) * 2);
   std::vector<float> inv(hs / 2);
   for (int i = 0; i < hs; i += 2) {
-    inv[i / 2] = powf(10000.0f, -(float)i / (float)hs);
+    const float e = -(float)i / (float)hs;
+    inv[i / 2] = (float)pow(10000.0, (double)e);
   }
   for (int p = 0; p < c.seq_len; ++p) {
     for (int j = 0; j < hs / 2; ++j) {

@@ -49,6 +49,14 @@ bool flash_attn_fwd_launch(const uint16_t *q, const uint16_t *k,
  * a forced count applies where splitting is allowed). */
 void flash_attn_force_splits(int splits);
 
+/* Frees, in `stream`'s order, the key-split workspace kept for `stream` on
+ * any device (nothing for the default stream or a stream that is capturing);
+ * returns the blocks freed. The stream must still exist. */
+int flash_attn_release_stream(hipStream_t stream);
+
+/* Split workspaces currently held, and their bytes. */
+void flash_attn_workspace_stats(int64_t *blocks, int64_t *bytes);
+
 } // namespace vxk
 
 #endif /* VX_AMD_OPS_KERNELS_H */

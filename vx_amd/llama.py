@@ -17,6 +17,8 @@ from __future__ import annotations
 
 from dataclasses import asdict, dataclass
 
+import math
+
 import numpy as np
 
 
@@ -72,16 +74,32 @@ def quantize_rows(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     return q, scale
 
 
+def rope_inv_freq(head_size: int) -> np.ndarray:
+    """10000^(-i/hs) for even i as the reference's f32 `powf` gives it
+    (reference tests/modules/llama_rt.vx:82-85; stdlib/core/num.vx:2476-2479
+    documents powf as correctly rounded): the exponent -(i as f32) / (hs as
+    f32) in f32, the power in double (glibc's pow, under 1 ulp of double),
+    rounded to f32 once."""
+    e = [float(-np.float32(i) / np.float32(head_size)) for i in range(0, head_size, 2)]
+    return np.array([math.pow(10000.0, x) for x in e], np.float64).astype(np.float32)
+
+
 def rope_table(cfg: LlamaConfig, positions: int | None = None) -> np.ndarray:
-    """[positions, head_size / 2, 2] of (cos, sin) of pos * 10000^(-i/hs)
-    for even i, the angle in f32 as the reference computes it."""
+    """[positions, head_size / 2, 2] of (cos, sin) of the f32 angle
+    (pos as f32) * rope_inv_freq, as reference examples/llama.vx:244-246
+    computes them: f32 `cos`/`sin`, which reference stdlib/core/num.vx:2434-2442
+    documents as correctly rounded. Each is the double cos/sin of the f32
+    angle (glibc, under 1 ulp of double) rounded to f32 once; a CPU test
+    checks every entry against a 60-digit evaluation where the rounding is
+    close."""
     positions = cfg.seq_len if positions is None else positions
     hs = cfg.head_size
-    i = np.arange(0, hs, 2, dtype=np.float32)
-    inv = np.power(np.float32(10000.0), -i / np.float32(hs)).astype(np.float32)
+    inv = rope_inv_freq(hs)
     pos = np.arange(positions, dtype=np.float32)[:, None]
     ang = (pos * inv[None, :]).astype(np.float32).astype(np.float64)
-    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+    cos = np.vectorize(math.cos, otypes=[np.float64])(ang)
+    sin = np.vectorize(math.sin, otypes=[np.float64])(ang)
+    return np.stack([cos, sin], axis=-1).astype(np.float32)
 
 
 def make_model(cfg: LlamaConfig, seed: int = 0) -> dict[str, np.ndarray]:
