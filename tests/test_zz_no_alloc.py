@@ -142,15 +142,15 @@ def test_noalloc_calls_on_two_streams_take_turns(hiplib, rng):
 
     announce("noalloc GEMM: two streams, host bf16 operands 512x2048x1024 each")
     t = HipTimer()
+    cases = [(f32_to_bf16(rng.normal(0, 1 / 32, (512, 2048)).astype(np.float32)),
+              f32_to_bf16(rng.normal(0, 1 / 32, (2048, 1024)).astype(np.float32)))
+             for _ in range(2)]
+    # results allocated with no stream set (memory taken while a stream is
+    # set is freed in that stream's order, so it must go before the stream)
+    outs = [DeviceArray(hiplib, (512, 1024), abi.DTYPE_F32) for _ in cases]
     streams = [t.stream_create(), t.stream_create()]
-    cases, outs = [], []
     try:
-        for i, s in enumerate(streams):
-            a16 = f32_to_bf16(rng.normal(0, 1 / 32, (512, 2048)).astype(np.float32))
-            b16 = f32_to_bf16(rng.normal(0, 1 / 32, (2048, 1024)).astype(np.float32))
-            c = DeviceArray(hiplib, (512, 1024), abi.DTYPE_F32)
-            cases.append((a16, b16))
-            outs.append(c)
+        for (a16, b16), c, s in zip(cases, outs, streams):
             hiplib.lib.vx_hip_set_stream(s)
             assert noalloc(hiplib, abi.matmul_payload(),
                            gemm_args(a16, abi.DTYPE_BF16, b16, abi.DTYPE_BF16, c,
@@ -164,7 +164,7 @@ def test_noalloc_calls_on_two_streams_take_turns(hiplib, rng):
     finally:
         hiplib.lib.vx_hip_set_stream(None)
         t.sync()
-        for s in streams:
-            t.stream_destroy(s)
         for c in outs:
             c.free()
+        for s in streams:
+            t.stream_destroy(s)

@@ -29,6 +29,7 @@
 #include "../../../include/vx_hardware_runtime.h"
 #include "../vx_hip_common.h"
 #include "../vx_kernels.h"
+#include "gemm_pp_layout.h"
 
 #include <type_traits>
 
@@ -41,16 +42,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kTileM = 256;
-constexpr int kTileN = 256;
-/* Tile rows per launch-order group: 4, and 2 for grids of at most one
- * round (256 tiles). Measured on the ping-pong kernel (bf16 -> f32, paired
- * runs on one box): 4096^3 with groups of 1, 2, 4 and 16 rows 1231-1235,
- * 1231-1235, 1196-1201 and 1220-1230 TFLOP/s; 8192^3 with 2, 4, 8 and 16
- * rows 1240-1254, 1282-1290, 1269-1280 and 1248-1255. */
-constexpr int kGroupM = 4;
-constexpr int kSmallGrid = 256;
-constexpr int kSmallGroupM = 2;
+constexpr int kTileM = pp::kTileM;
+constexpr int kTileN = pp::kTileN;
+/* Launch order (pp::tile_of): tile rows per group 4, and 2 for grids of at
+ * most one round (256 tiles). Measured on the ping-pong kernel (bf16 -> f32,
+ * paired runs on one box): 4096^3 with groups of 1, 2, 4 and 16 rows
+ * 1231-1235, 1231-1235, 1196-1201 and 1220-1230 TFLOP/s; 8192^3 with 2, 4, 8
+ * and 16 rows 1240-1254, 1282-1290, 1269-1280 and 1248-1255. */
 
 template <int kOut>
 __device__ __forceinline__ void put(void *c, int64_t at, float v) {
@@ -84,17 +82,13 @@ __device__ __forceinline__ void put(void *c, int64_t at, float v) {
  *
  * The buffer descriptors bound each load to the operand's extent, so an
  * offset past it reads zeros instead of faulting. */
-constexpr int kDStageK = 32;
-constexpr int kDUnits = kTileM * kDStageK / 8; /* 16-byte units per plane */
+constexpr int kDStageK = pp::kStageK;
+constexpr int kDUnits = pp::kUnits; /* 16-byte units per plane */
 constexpr int kBufferFlags = 0x00020000;       /* raw 32-bit dwords */
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 #define VX_LDS __attribute__((address_space(3)))
-
-__device__ __forceinline__ int dswz_a(int row, int c) {
-  return c ^ (((row >> 1) ^ (row >> 2)) & 3);
-}
 
 /* Wait until at most `n` of this wave's vector memory operations are
  * outstanding (vmcnt n; lgkmcnt and expcnt untouched). */
@@ -194,9 +188,6 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void *base, int bytes) {
  * transposing read touches land in distinct banks. Each accumulator adds its
  * 32-term stage sums in k order, so results are deterministic (not
  * bit-identical to the 32x32x16 kernels, which add 16-term sums). */
-__device__ __forceinline__ int pswz_b(int k, int c) {
-  return c ^ (((k & 3) | (((k >> 3) & 1) << 2)) << 1);
-}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -229,26 +220,16 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     clk0 = __builtin_amdgcn_s_memtime();
     rt0 = __builtin_amdgcn_s_memrealtime();
   }
-  constexpr int kLoads = kDUnits / 64 / 8; /* per wave per plane */
-  constexpr int kTM = 8;                   /* 16-row blocks per wave */
-  constexpr int kTN = 4;                   /* 16-column blocks per wave */
+  constexpr int kLoads = pp::kLoads; /* per wave per plane */
+  constexpr int kTM = pp::kTM;       /* 16-row blocks per wave */
+  constexpr int kTN = pp::kTN;       /* 16-column blocks per wave */
+  static_assert(kNS == pp::kSlots, "ring depth");
   __shared__ u32x4 ring[kNS][2][kDUnits];
 
   const int t = threadIdx.x;
-  int id = blockIdx.x;
-  const int nwg = gridDim.x;
-  if ((nwg & 7) == 0) {
-    id = (id & 7) * (nwg >> 3) + (id >> 3);
-  }
-  const int group_m = tiles_m * tiles_n <= kSmallGrid ? kSmallGroupM : kGroupM;
-  const int group_size = group_m * tiles_n;
-  const int first_m = (id / group_size) * group_m;
-  const int rows_in_group = min(tiles_m - first_m, group_m);
-  const int in_group = id % group_size;
-  const int tm = first_m + in_group % rows_in_group;
-  const int tn = in_group / rows_in_group;
-  const int64_t m0 = (int64_t)tm * kTileM;
-  const int64_t n0 = (int64_t)tn * kTileN;
+  const pp::Tile tile = pp::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n);
+  const int64_t m0 = (int64_t)tile.tm * kTileM;
+  const int64_t n0 = (int64_t)tile.tn * kTileN;
 
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lane = t & 63;
@@ -256,38 +237,28 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
   uint32_t a_off[kLoads], b_off[kLoads];
 #pragma unroll
   for (int p = 0; p < kLoads; ++p) {
-    const int u = (wave * kLoads + p) * 64 + lane;
-    const int arow = u >> 2;
-    a_off[p] = (uint32_t)(arow * lda * 2 + dswz_a(arow, u & 3) * 16);
-    const int bk = u >> 5;
-    b_off[p] = (uint32_t)(bk * ldb * 2 + pswz_b(bk, u & 31) * 16);
+    a_off[p] = pp::a_load_off(wave, p, lane, lda);
+    b_off[p] = pp::b_load_off(wave, p, lane, ldb);
   }
   /* A stage's loads cover a 256 x 32 block of A and a 32 x 256 block of B;
    * each buffer ends at the last element of its matrix, so rows of A past M
    * and the tail of B's last row read zeros. Columns of B past N within
    * earlier rows read whatever follows them, which only reaches outputs past
    * N, and those are not stored. */
-  const int64_t a_full = (kTileM - 1) * lda * 2 + kDStageK * 2;
-  const int64_t b_full = (kDStageK - 1) * ldb * 2 + kTileN * 2;
-  const int64_t a_end = ((M - 1) * lda + K) * 2; /* bytes from A */
-  const int64_t b_end = ((int64_t)(K - 1) * ldb + N) * 2;
-
   const uint32_t ring_base =
       (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
   auto issue = [&](int step, int slot) {
-    const int64_t a0 = m0 * lda + (int64_t)step * kDStageK;
-    const int64_t b0 = (int64_t)step * kDStageK * ldb + n0;
-    const i32x4 ra = buffer_rsrc(A + a0, (int)min(a_full, a_end - a0 * 2));
-    const i32x4 rb = buffer_rsrc(B + b0, (int)min(b_full, b_end - b0 * 2));
-    const uint32_t la = ring_base + (uint32_t)(slot * 2 * kDUnits * 16) +
-                        (uint32_t)(wave * kLoads * 64 * 16);
+    const int64_t a0 = pp::a_stage_base(m0, lda, step);
+    const int64_t b0 = pp::b_stage_base(n0, ldb, step);
+    const i32x4 ra = buffer_rsrc(A + a0, pp::a_stage_bytes(M, K, lda, a0));
+    const i32x4 rb = buffer_rsrc(B + b0, pp::b_stage_bytes(N, K, ldb, b0));
 #pragma unroll
     for (int p = 0; p < kLoads; ++p) {
-      dma16(ra, a_off[p], la + p * 64 * 16);
+      dma16(ra, a_off[p], ring_base + pp::lds_a_dst(slot, wave, p));
     }
 #pragma unroll
     for (int p = 0; p < kLoads; ++p) {
-      dma16(rb, b_off[p], la + kDUnits * 16 + p * 64 * 16);
+      dma16(rb, b_off[p], ring_base + pp::lds_b_dst(slot, wave, p));
     }
   };
 
@@ -310,16 +281,13 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     const VX_LDS char *lb = (const VX_LDS char *)&ring[slot][1][0];
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
-      const int row = wm * 128 + i * 16 + l16;
-      af[i] = la[row * 4 + dswz_a(row, kc)];
+      af[i] = la[pp::lds_a_read(wm, i, l16, kc)];
     }
 #pragma unroll
     for (int j = 0; j < kTN; ++j) {
-      const int n = wn * 64 + j * 16 + 4 * (l16 & 3);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int k = 8 * kc + 4 * h + (l16 >> 2);
-        const int at = k * (kTileN * 2) + pswz_b(k, n >> 3) * 16 + (n & 7) * 2;
+        const int at = pp::lds_b_read(wn, j, h, l16, kc);
         const u32x2 w = __builtin_bit_cast(
             u32x2,
             __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS i16x4 *)(lb + at)));
@@ -372,10 +340,10 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
   for (int i = 0; i < kTM; ++i) {
 #pragma unroll
     for (int jj = 0; jj < kTN; ++jj) {
-      const int64_t col = n0 + wn * 64 + jj * 16 + l16;
+      const int64_t col = n0 + pp::c_col(wn, jj, l16);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + wm * 128 + i * 16 + 4 * kc + r;
+        const int64_t row = m0 + pp::c_row(wm, i, r, kc);
         if (row < M && col < N) {
           put<kOut>(C, row * ldc + col, acc[i][jj][r]);
         }
@@ -662,16 +630,8 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 bool pp_takes(const GemmArgs &g) {
   const bool sixteen = g.in_dtype == VX_DTYPE_BF16 || g.in_dtype == VX_DTYPE_F16;
   const bool out_ok = g.out_dtype == VX_DTYPE_F32 || g.out_dtype == g.in_dtype;
-  if (!sixteen || !out_ok || g.m <= 0 || g.n <= 0 || g.k <= 0 ||
-      g.k % kDStageK != 0 || g.k > INT32_MAX || g.n % 8 != 0 || g.lda % 8 != 0 ||
-      g.ldb % 8 != 0 || g.lda < g.k || g.ldb < g.n || g.ldc < g.n ||
-      !aligned16(g.a) || !aligned16(g.b)) {
-    return false;
-  }
-  const int64_t tiles = ((g.m + kTileM - 1) / kTileM) * ((g.n + kTileN - 1) / kTileN);
-  return tiles <= INT32_MAX &&
-         (kTileM - 1) * g.lda * 2 + kDStageK * 2 <= INT32_MAX &&
-         (kDStageK - 1) * g.ldb * 2 + kTileN * 2 <= INT32_MAX;
+  return sixteen && out_ok && aligned16(g.a) && aligned16(g.b) &&
+         pp::shape_ok(g.m, g.n, g.k, g.lda, g.ldb, g.ldc);
 }
 
 bool f32_mfma_takes(const GemmArgs &g) {
