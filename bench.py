@@ -46,13 +46,14 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def traffic_from_profiles(name: str):
-    """HBM bytes per launch measured with rocprofv3 PMC counters, committed
-    as profiles/<name>_traffic.json; None when not measured."""
+def traffic_from_profiles(name: str, key: str = "bytes_per_launch"):
+    """HBM bytes per launch (or per decode position) measured with rocprofv3
+    PMC counters, committed as profiles/<name>_traffic.json; None when not
+    measured."""
     p = ROOT / "profiles" / f"{name}_traffic.json"
     if p.exists():
         try:
-            return json.loads(p.read_text()).get("bytes_per_launch")
+            return json.loads(p.read_text()).get(key)
         except (ValueError, OSError):
             return None
     return None
@@ -112,9 +113,12 @@ def settle(call, timer, min_ms: float = SETTLE_MS) -> float:
 
 
 def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None = None,
-               k: int | None = None):
+               k: int | None = None, runs: int = 3):
     """C[m, n] = A[m, k] B[k, n] (m = k = n unless given), bf16 in, f32
-    out, through vx_plugin_dispatch_async."""
+    out, through vx_plugin_dispatch_async. `runs` timed regions of `steps`
+    dispatches each (hipEvents around each region); the rate is the median
+    region's, and every region is kept in `runs_us` (per-step median, fastest
+    and slowest region)."""
     from vx_amd import abi
     from vx_amd.abi import f32_to_bf16
     from vx_amd.runtime import DeviceArray, matmul
@@ -149,17 +153,20 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
     timer.sync()
     # Clock stamps of the timed launches (workgroup 0's shader-clock and
     # 100 MHz real-time counters at its start and end), one slot per step.
-    stamps = lib.transfer(None, 32 * steps)
-    lib.clock_stamps(stamps, steps)
-    e0, e1 = timer.event(), timer.event()
+    stamps = lib.transfer(None, 32 * steps * runs)
+    lib.clock_stamps(stamps, steps * runs)
+    region_ms = []
     t0 = time.perf_counter()
-    timer.record(e0)
-    for i in range(steps):
-        dispatch(buf, len(pl), argv, tags, nargs)
-    timer.record(e1)
-    ms_events = timer.elapsed_ms(e0, e1)
+    for _ in range(runs):
+        e0, e1 = timer.event(), timer.event()
+        timer.record(e0)
+        for i in range(steps):
+            dispatch(buf, len(pl), argv, tags, nargs)
+        timer.record(e1)
+        region_ms.append(timer.elapsed_ms(e0, e1))
     timer.sync()
     wall = time.perf_counter() - t0
+    ms_events = float(np.median(region_ms))
     lib.clock_stamps(None, 0)
     # The spread: the same steps again, each bracketed by its own events (an
     # event between two launches can delay the second, so these do not
@@ -171,14 +178,14 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
         timer.record(events[i + 1])
     timer.sync()
     step_ms = [timer.elapsed_ms(events[i], events[i + 1]) for i in range(steps)]
-    st = np.empty((steps, 4), np.uint64)
+    st = np.empty((steps * runs, 4), np.uint64)
     lib.fetch(stamps, st)
     lib.free(stamps)
     clk = (st[:, 2] - st[:, 0]).astype(np.float64)
     rt = (st[:, 3] - st[:, 1]).astype(np.float64)
     clock_mhz = float(clk.sum() / rt.sum() * 100.0) if rt.sum() > 0 else None
     after = lib.stats()
-    assert after["gemm_mfma"] - before["gemm_mfma"] == 2 * steps + warmup + settled[0], \
+    assert after["gemm_mfma"] - before["gemm_mfma"] == (runs + 1) * steps + warmup + settled[0], \
         "GEMM did not take the MFMA path"
     c = dc.numpy()
     assert np.isfinite(c).all()
@@ -186,8 +193,10 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
         x.free()
     flops = 2.0 * m * n * k
     ms_step = ms_events / steps
-    return dict(n=n, m=m, k=k, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / steps,
+    return dict(n=n, m=m, k=k, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / (steps * runs),
                 tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16,
+                runs_us=spread([x * 1e3 / steps for x in region_ms]),
+                tflops_runs=spread([flops / (x / steps * 1e-3) / 1e12 for x in region_ms]),
                 steps_us=spread([x * 1e3 for x in step_ms]), clock_mhz=clock_mhz)
 
 
@@ -480,40 +489,80 @@ def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
                        f"{dt:.1f} s), oracle/vx_oracle.c loop nest, 1 thread")
 
 
-def copy_ceiling(lib, timer, sizes) -> dict:
-    """A measured streaming ceiling beside the 8 TB/s nameplate: the HIP
-    runtime's device-to-device copy (read n bytes, write n bytes) of each
-    size, rotating through enough buffer pairs (over 1 GiB) that every copy
-    streams from and to HBM rather than the 256 MB MALL; 12 copies per timed
-    region, three regions. GB/s counts the bytes read plus written.
-    `sizes` maps a name to a byte count."""
+def read_ceiling(lib, timer, sizes) -> dict:
+    """The measured HBM read ceiling beside the 8 TB/s nameplate: one
+    dispatch of vx_amd/probes/read_probe.hip (each workgroup reads one
+    contiguous burst, every load issued before any is used) over n bytes,
+    for each size, at bursts of 16, 32 and 64 KiB per workgroup with plain
+    and non-temporal loads; the fastest is the ceiling. Like the GEMV entries, each size rotates through
+    enough buffers (over 1 GiB) that every dispatch streams from HBM rather
+    than the 256 MB MALL, and is timed as hipGraph replays (four, per-call
+    median) so the host's launch rate does not enter. GB/s counts the bytes
+    read. `sizes` maps a name to a byte count (a multiple of 64 KiB)."""
     import ctypes
 
     hip = timer.hip
-    hip.hipMemcpyDtoDAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                       ctypes.c_void_p]
+    vp = ctypes.c_void_p
+    path = ROOT / "vx_amd" / "probes" / "read_probe.hsaco"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+    mod = vp()
+    hip.hipModuleLoad.argtypes = [ctypes.POINTER(vp), ctypes.c_char_p]
+    assert hip.hipModuleLoad(ctypes.byref(mod), str(path).encode()) == 0, "hipModuleLoad"
+    hip.hipModuleGetFunction.argtypes = [ctypes.POINTER(vp), vp, ctypes.c_char_p]
+    hip.hipModuleLaunchKernel.argtypes = [vp] + [ctypes.c_uint] * 7 + [vp, ctypes.POINTER(vp), vp]
+    funcs = {}
+    for units in (4, 8, 16):
+        for aux in (0, 2):
+            f = vp()
+            assert hip.hipModuleGetFunction(ctypes.byref(f), mod,
+                                            f"vx_read_probe_{units}_{aux}".encode()) == 0
+            funcs[(units, aux)] = f
+    stream = timer.stream_create()
     out = {}
-    for name, nbytes in sizes.items():
-        pairs = max(4, -(-2**30 // (2 * nbytes)))
-        bufs = [(lib.transfer(None, nbytes), lib.transfer(None, nbytes)) for _ in range(pairs)]
-        turn = [0]
+    try:
+        for name, nbytes in sizes.items():
+            assert nbytes % (64 * 1024) == 0, name
+            copies = max(4, -(-2**30 // nbytes))
+            bufs = [lib.transfer(None, nbytes) for _ in range(copies)]
+            sink = lib.transfer(None, nbytes // 4)  # the store a probe never makes
+            best = None
+            for (units, aux), f in funcs.items():
+                grid = nbytes // (256 * units * 16)
+                params = [(vp(b), vp(sink)) for b in bufs]
+                arrays = [(ctypes.c_void_p * 2)(ctypes.addressof(a), ctypes.addressof(o))
+                          for a, o in params]
 
-        def call():
-            src, dst = bufs[turn[0] % pairs]
-            turn[0] += 1
-            rc = hip.hipMemcpyDtoDAsync(dst, src, nbytes, None)
-            assert rc == 0, f"hipMemcpyDtoDAsync failed with {rc}"
+                def calls():
+                    for arr in arrays:
+                        rc = hip.hipModuleLaunchKernel(f, grid, 1, 1, 256, 1, 1, 0, stream,
+                                                       ctypes.cast(arr, ctypes.POINTER(vp)), None)
+                        assert rc == 0, f"hipModuleLaunchKernel failed with {rc}"
 
-        for _ in range(pairs):
-            call()
+                graph = timer.capture(stream, calls)
+                timer.graph_launch(graph, stream)  # warm
+                reps = 4
+                ev = [timer.event() for _ in range(reps + 1)]
+                timer.record(ev[0], stream)
+                for r in range(reps):
+                    timer.graph_launch(graph, stream)
+                    timer.record(ev[r + 1], stream)
+                per_rep = [timer.elapsed_ms(ev[r], ev[r + 1]) / copies * 1e3 for r in range(reps)]
+                timer.graph_destroy(graph)
+                us = float(np.median(per_rep))
+                row = dict(bytes=nbytes, burst_kib=units * 4, nontemporal=aux == 2, us=round(us, 3),
+                           gbs=round(nbytes / (us * 1e-6) / 1e9, 1), runs_us=spread(per_rep),
+                           rotated_copies=copies)
+                if best is None or row["us"] < best["us"]:
+                    best = row
+            out[name] = best
+            for b in bufs + [sink]:
+                lib.free(b)
+    finally:
         timer.sync()
-        runs = timed_runs(call, timer, 12)
-        us = float(np.median(runs)) * 1e3
-        out[name] = dict(bytes=nbytes, us=round(us, 3), gbs=round(2 * nbytes / (us * 1e-6) / 1e9, 1),
-                         runs_us=spread([x * 1e3 for x in runs]), rotated_pairs=pairs)
-        for src, dst in bufs:
-            lib.free(src)
-            lib.free(dst)
+        timer.stream_destroy(stream)
+        hip.hipModuleUnload.argtypes = [vp]
+        hip.hipModuleUnload(mod)
     return out
 
 
@@ -577,16 +626,22 @@ def main() -> int:
     if "gemv" in only:
         log("int8 gemv config 5")
         extra["gemv_i8"] = bench_gemv(lib, timer, max(20, ns.steps), 3)
-        # the weight bytes of each shape copied device to device: what one
-        # dispatch streaming that many bytes reaches on this box
-        ceil = copy_ceiling(lib, timer, {"4096x4096": 4096 * 4096, "11008x4096": 11008 * 4096,
+        # what one dispatch reading each shape's weight bytes reaches on this
+        # box (the single-dispatch burst read), beside the nameplate
+        ceil = read_ceiling(lib, timer, {"4096x4096": 4096 * 4096, "11008x4096": 11008 * 4096,
                                          "256MiB": 256 * 2**20})
-        extra["hbm_copy_ceiling"] = ceil
+        extra["hbm_read_ceiling"] = ceil
         for r in extra["gemv_i8"]:
-            # 11008x4096 and 4096x11008 stream the same 45.1 MB of weights
+            # 11008x4096 and 4096x11008 stream the same 45.1 MB of weights;
+            # the ceiling reads the weight bytes alone
             c = ceil["4096x4096" if r["shape"] == [4096, 4096] else "11008x4096"]
-            r["roofline"]["copy_ceiling_gbs"] = c["gbs"]
-            r["roofline"]["frac_of_copy_ceiling"] = round(r["gbs"] / c["gbs"], 4)
+            r["roofline"]["read_ceiling_us"] = c["us"]
+            r["roofline"]["read_ceiling_gbs"] = c["gbs"]
+            r["roofline"]["frac_of_read_ceiling"] = round(c["us"] / r["us"], 4)
+        b1 = {tuple(r["shape"]): r["us"] for r in extra["gemv_i8"] if r["batch"] == 1}
+        for r in extra["gemv_i8"]:
+            # the cost of the batch: this call's time over the batch-1 call's
+            r["vs_batch1"] = round(r["us"] / b1[tuple(r["shape"])], 3)
         log("gemv " + ", ".join(f"{r['shape'][0]}x{r['shape'][1]}b{r['batch']}:{r['gbs']:.0f}GB/s"
                                 for r in extra["gemv_i8"]))
     if "decode" in only:
@@ -598,7 +653,8 @@ def main() -> int:
         # rows it reads and writes) over the whole generate call's time
         dec["roofline"] = {"bound": "hbm", "achieved": round(dec["bytes_gbs"], 1),
                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                           "frac": round(dec["bytes_gbs"] / PEAK_HBM_GBS, 4), "traffic": None}
+                           "frac": round(dec["bytes_gbs"] / PEAK_HBM_GBS, 4),
+                           "traffic": traffic_from_profiles("decode_i8", "bytes_per_position")}
         extra["decode_i8"] = dec
 
     if "gemm" in only:
@@ -654,6 +710,8 @@ def main() -> int:
         "config": {"workload": "bf16 x bf16 -> f32 GEMM, M=N=K=4096 (BASELINE config 2), "
                                "operands resident in HBM, one vx_plugin_dispatch_async per step",
                    "m": 4096, "n": 4096, "k": 4096},
+        "runs_us": g["runs_us"],
+        "tflops_runs": g["tflops_runs"],
         "steps_us": g["steps_us"],
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),

@@ -142,6 +142,33 @@ def test_baseline_config_sampled(hiplib):
         assert_max_abs(lse[bi, hi], wl_head, 1e-3, f"config 3 whole head lse ({bi}, {hi})")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("rise", [320.0, 1024.0, -1024.0])
+def test_scores_rising_after_the_first_block(hiplib, causal, rise, rng):
+    """Keys 64 and up score `rise` above keys 0-63 for every query (q and k
+    share a large first component), so a row's first key block sets a
+    reference far below its true max. At 320 the rise is 40.8 in base-2
+    exponent units (scale 1/sqrt(128) times log2(e)): p reaches 2^41 and the
+    sums stay finite. At 1024 it is 130.6: p overflows, the sums pass 2^64
+    and the workgroup redoes its rows with the moving max. At -1024 the later
+    keys all but vanish. Every row against the f64 oracle."""
+    announce(f"flash attn score rise {rise} causal={causal}")
+    b, h, s, d = 1, 2, 320, 128
+    q = rng.standard_normal((b, h, s, d)).astype(np.float32) * 0.1
+    k = rng.standard_normal((b, h, s, d)).astype(np.float32) * 0.1
+    v = rng.standard_normal((b, h, s, d)).astype(np.float32)
+    q[..., 0] = 32.0
+    k[..., :64, 0] = 0.0
+    k[..., 64:, 0] = rise / 32.0
+    q16, k16, v16 = f32_to_bf16(q), f32_to_bf16(k), f32_to_bf16(v)
+    scale = 1.0 / np.sqrt(d)
+    o, lse = run(hiplib, q16, k16, v16, h, h, scale, causal, poison=True)
+    rows = oracle.attention_all_rows(b, h, s)
+    wo, wl = oracle.attention_rows(q16, k16, v16, h, h, scale, causal, rows)
+    assert_max_abs(o.reshape(-1, d), wo, BF16_ABS, f"rise {rise}")
+    assert_max_abs(lse.ravel(), wl, 1e-3, f"rise {rise} lse")
+
+
 @pytest.mark.parametrize("start", [0, 1536, 7680])
 def test_reference_prefill_chunks(hiplib, start):
     """The reference's own flash-attention benchmark shape (reference

@@ -124,6 +124,28 @@ def build_test_images(verbose: bool = False) -> list[Path]:
     return out
 
 
+PROBES = PKG / "probes"
+
+
+def build_probes(verbose: bool = False) -> list[Path]:
+    """Measurement kernels that are not part of the library (the HBM read
+    ceiling bench.py reports): each vx_amd/probes/*.hip as a bare gfx950 code
+    object next to its source."""
+    out = []
+    for src in sorted(PROBES.glob("*.hip")):
+        dst = src.with_suffix(".hsaco")
+        cmd = [hipcc(), "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               "--no-gpu-bundle-output", str(src), "-o", str(dst)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"compiling {src.name} failed:\n{res.stderr}")
+        out.append(dst)
+    return out
+
+
 def build_oracle(verbose: bool = False) -> None:
     """The CPU checker (oracle/liboracle.so) and, where the reference checkout
     exists, oracle/_ref/libvx_x86_dispatch.so built from its sources."""
@@ -137,4 +159,5 @@ def build_oracle(verbose: bool = False) -> None:
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
     build_test_images(verbose="-v" in sys.argv)
+    build_probes(verbose="-v" in sys.argv)
     build_oracle(verbose="-v" in sys.argv)
