@@ -146,12 +146,13 @@ def test_baseline_config_sampled(hiplib):
 @pytest.mark.parametrize("rise", [320.0, 1024.0, -1024.0])
 def test_scores_rising_after_the_first_block(hiplib, causal, rise, rng):
     """Keys 64 and up score `rise` above keys 0-63 for every query (q and k
-    share a large first component), so a row's first key block sets a
-    reference far below its true max. At 320 the rise is 40.8 in base-2
-    exponent units (scale 1/sqrt(128) times log2(e)): p reaches 2^41 and the
-    sums stay finite. At 1024 it is 130.6: p overflows, the sums pass 2^64
-    and the workgroup redoes its rows with the moving max. At -1024 the later
-    keys all but vanish. Every row against the f64 oracle."""
+    share a large first component), so the running max a row takes from its
+    first key block is far below its true max. At 320 the rise is 40.8 in
+    base-2 exponent units (scale 1/sqrt(128) times log2(e)); at 1024 it is
+    130.6, past f32's exponent range were p not taken against the moved
+    max: the reference max moves, O and l are rescaled, and the first
+    block's terms vanish. At -1024 the later keys all but vanish. Every row
+    against the f64 oracle."""
     announce(f"flash attn score rise {rise} causal={causal}")
     b, h, s, d = 1, 2, 320, 128
     q = rng.standard_normal((b, h, s, d)).astype(np.float32) * 0.1

@@ -65,6 +65,18 @@ def test_same_plugin_symbols_as_reference_library():
     assert ref <= ours, f"reference exports we lack: {sorted(ref - ours)}"
 
 
+def test_exports_only_the_c_abi():
+    """Every dynamic symbol the library defines is part of the C ABI (vx_*):
+    its C++ internals stay local, so two libraries loaded into one process
+    (two builds of this one, or another with the same C++ names) never bind
+    to each other's internals."""
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    names = [ln.split()[-1] for ln in out.splitlines() if ln.strip()]
+    assert names and all(n.startswith("vx_") for n in names), \
+        sorted(n for n in names if not n.startswith("vx_"))[:10]
+
+
 def gpu_present(lib) -> bool:
     return lib.device_count() > 0
 

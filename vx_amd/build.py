@@ -89,6 +89,7 @@ def build(verbose: bool = False) -> Path:
         str(FFI_LIB),
         "-ldl",
         "-lpthread",
+        f"-Wl,--version-script={CSRC / 'exports.map'}",
     ]
     if verbose:
         print(" ".join(cmd), flush=True)

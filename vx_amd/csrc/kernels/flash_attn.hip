@@ -89,13 +89,6 @@ constexpr int kThreads = 256;
 #define VX_FA_PV_LEAD 8
 #endif
 constexpr float kSlack = 8.0f; /* base-2 headroom of the stale row max */
-/* 1: each row keeps the reference max its first key block gives (no row max,
- * no rescale of O in the loop; a workgroup whose sums pass kRefLimit redoes
- * its rows with the moving max). 0: the moving reference with kSlack. */
-#ifndef VX_FA_FIXREF
-#define VX_FA_FIXREF 1
-#endif
-constexpr float kRefLimit = 18446744073709551616.0f; /* 2^64 */
 /* Heads an XCD works through together (0: all of its heads at once). */
 #ifndef VX_FA_HG
 #define VX_FA_HG 4
@@ -363,45 +356,15 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
   };
 
   const float hide = scale_log2 >= 0.0f ? -INFINITY : INFINITY;
-  using T = std::true_type;
-  using F = std::false_type;
 
   /* Softmax of one query tile's raw scores against its running reference
    * max: the P^T operands in `pt`, the factor O and l take, and whether the
    * reference moved. Masked scores are +-inf (the scale's sign) in raw form
    * and come out as exactly 0. */
   auto softmax = [&](Scores &st, int qt, u32x4 (&pt)[kKS], float &alpha,
-                     auto masked, auto pos, auto first_block) -> bool {
+                     auto masked, auto pos) -> bool {
     constexpr bool kMasked = decltype(masked)::value;
     constexpr bool kPos = decltype(pos)::value;
-    if constexpr (VX_FA_FIXREF != 0 && !decltype(first_block)::value) {
-      /* The reference max stays where the row's first block put it. */
-      alpha = 1.0f;
-      float psum = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < kKT; ++kt) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float p[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = st[kt][qt][8 * hh + e];
-            p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x, scale_log2, -m_run[qt]));
-            if constexpr (kMasked) {
-              p[e] = x == hide ? 0.0f : p[e];
-            }
-            psum += p[e];
-          }
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            pt[2 * kt + hh][w] = pack2(p[2 * w], p[2 * w + 1]);
-          }
-        }
-      }
-      const auto r = halves(psum);
-      l_run[qt] += r[0] + r[1];
-      return false;
-    }
     float ext = kPos ? -INFINITY : INFINITY;
 #pragma unroll
     for (int kt = 0; kt < kKT; ++kt) {
@@ -418,13 +381,10 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     /* The reference max m moves only when a block's max passes it by more
      * than kSlack (and always from -inf): p = 2^(s - m) then stays below
      * 2^kSlack, and O and l share the stale m, so the result is the same up
-     * to rounding while most blocks skip the O rescale. (With a fixed
-     * reference this runs on a row's first block only, from -inf.) */
+     * to rounding while most blocks skip the O rescale. */
     const bool bump = mx > m_run[qt] + kSlack;
     const float m_next = bump ? mx : m_run[qt];
-    /* All keys so far masked: keep exponents finite (everything is 0). With
-     * a fixed reference the row then sees no key of this launch's range, so
-     * 0 stays its reference. */
+    /* All keys so far masked: keep exponents finite (everything is 0). */
     const float m_use = m_next == -INFINITY ? 0.0f : m_next;
     alpha = bump ? __builtin_amdgcn_exp2f(m_run[qt] - m_use) : 1.0f;
     float psum = 0.0f;
@@ -534,15 +494,15 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     const bool need_mask =
         key0 + kBlockK > seq_k || (causal && key0 + kBlockK - 1 > qw0 + shift);
     const bool next = blk + 1 < nblocks && key0 + kBlockK <= wave_last;
-    const bool first_block = VX_FA_FIXREF != 0 && blk == first;
     u32x4 pt[kQT][kKS];
     float alpha[kQT];
     bool bump[kQT];
-    if (!need_mask && next && scale_log2 >= 0.0f && !first_block) {
+    if (!need_mask && next && scale_log2 >= 0.0f) {
       scores(blk + 1, sn);
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
-        bump[qt] = softmax(st, qt, pt[qt], alpha[qt], F{}, T{}, F{});
+        bump[qt] = softmax(st, qt, pt[qt], alpha[qt], std::false_type{},
+                           std::true_type{});
       }
 #if VX_FA_SGB > 0
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0); /* DS read */
@@ -573,30 +533,18 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
               st[kt][qt][r] = key <= limit ? st[kt][qt][r] : hide;
             }
           }
-          if (first_block) {
-            bump[qt] = scale_log2 >= 0.0f
-                           ? softmax(st, qt, pt[qt], alpha[qt], T{}, T{}, T{})
-                           : softmax(st, qt, pt[qt], alpha[qt], T{}, F{}, T{});
-          } else {
-            bump[qt] = scale_log2 >= 0.0f
-                           ? softmax(st, qt, pt[qt], alpha[qt], T{}, T{}, F{})
-                           : softmax(st, qt, pt[qt], alpha[qt], T{}, F{}, F{});
-          }
+          bump[qt] = scale_log2 >= 0.0f
+                         ? softmax(st, qt, pt[qt], alpha[qt], std::true_type{},
+                                   std::true_type{})
+                         : softmax(st, qt, pt[qt], alpha[qt], std::true_type{},
+                                   std::false_type{});
         }
       } else {
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
-          bump[qt] = first_block ? softmax(st, qt, pt[qt], alpha[qt], F{}, T{}, T{})
-                                 : softmax(st, qt, pt[qt], alpha[qt], F{}, T{}, F{});
+          bump[qt] = softmax(st, qt, pt[qt], alpha[qt], std::false_type{},
+                             std::true_type{});
         }
-      }
-    }
-    if constexpr (VX_FA_FIXREF != 0) {
-      /* O is never rescaled: on a row's first block it is still 0, and the
-       * reference does not move after it (the compiler drops the branch). */
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        bump[qt] = false;
       }
     }
     accumulate(blk, pt, alpha, bump);
@@ -619,75 +567,6 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
     step(blk, sa, sb);
     if (blk + 1 < nblocks) {
       step(blk + 1, sb, sa);
-    }
-  }
-
-  if constexpr (VX_FA_FIXREF != 0) {
-    /* A row whose sum passed kRefLimit (its scores rose far above its first
-     * block's, or the input holds inf or NaN) makes the workgroup redo all
-     * its rows, one block at a time, with the moving-max online softmax. */
-    __shared__ int redo_flag;
-    bool redo = false;
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) {
-      redo = redo || !(l_run[qt] <= kRefLimit);
-    }
-    if (t == 0) {
-      redo_flag = 0;
-    }
-    __syncthreads();
-    if (__builtin_amdgcn_ballot_w64(redo) != 0 && lane == 0) {
-      redo_flag = 1;
-    }
-    __syncthreads();
-    if (redo_flag != 0) {
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        m_run[qt] = -INFINITY;
-        l_run[qt] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kDTiles; ++i) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            o_acc[qt][i][r] = 0.0f;
-          }
-        }
-      }
-      for (int blk = first; blk < nblocks; ++blk) {
-        lds_barrier(); /* every wave is done with the slot */
-        issue(blk, 0);
-        issue(blk, 1);
-        wait_all_loads();
-        lds_barrier();
-        const int key0 = blk * kBlockK;
-        if (key0 > wave_last) {
-          continue;
-        }
-        Scores st;
-        scores(blk, st);
-        u32x4 pt[kQT][kKS];
-        float alpha[kQT];
-        bool bump[kQT];
-#pragma unroll
-        for (int qt = 0; qt < kQT; ++qt) {
-          const int my_q = qw0 + 32 * qt + lq;
-          const int limit = causal ? min(seq_k - 1, my_q + shift) : seq_k - 1;
-#pragma unroll
-          for (int kt = 0; kt < kKT; ++kt) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
-              st[kt][qt][r] = key <= limit ? st[kt][qt][r] : hide;
-            }
-          }
-          /* the moving max with no slack: every block rescales */
-          bump[qt] = scale_log2 >= 0.0f
-                         ? softmax(st, qt, pt[qt], alpha[qt], T{}, T{}, T{})
-                         : softmax(st, qt, pt[qt], alpha[qt], T{}, F{}, T{});
-          bump[qt] = true;
-        }
-        accumulate(blk, pt, alpha, bump);
-      }
     }
   }
 
