@@ -180,16 +180,24 @@ static void walk(const Shape &s) {
       for (int lane = 0; lane < 64; ++lane) {
         for (int i = 0; i < pp::kTM; ++i) {
           for (int jj = 0; jj < pp::kTN; ++jj) {
+            // the kernel's guard: the row and the first of the lane's 4
+            // columns; the 4 must then all lie in the row
+            const int64_t row = m0 + pp::c_row(wm, i, lane & 15);
+            const int64_t col0 = n0 + pp::c_col(wn, jj, lane >> 4);
+            if (!(row < s.m && col0 < s.n)) {
+              continue;
+            }
+            CHECK(col0 + 3 < s.n, "C columns %lld..+3 pass N", (long long)col0);
+            if (s.ldc % 4 == 0) {
+              CHECK((row * s.ldc + col0) % 4 == 0, "16-byte C store misaligned");
+            }
             for (int r = 0; r < 4; ++r) {
-              const int64_t row = m0 + pp::c_row(wm, i, r, lane >> 4);
-              const int64_t col = n0 + pp::c_col(wn, jj, lane & 15);
-              if (row < s.m && col < s.n) {
-                const int64_t at = row * s.ldc + col;
-                CHECK(at >= 0 && at < c_elems, "C store at %lld", (long long)at);
-                if (at >= 0 && at < c_elems) {
-                  CHECK(c_seen[(size_t)at]++ == 0, "C (%lld, %lld) stored twice", (long long)row,
-                        (long long)col);
-                }
+              const int64_t col = col0 + r;
+              const int64_t at = row * s.ldc + col;
+              CHECK(at >= 0 && at < c_elems, "C store at %lld", (long long)at);
+              if (at >= 0 && at < c_elems) {
+                CHECK(c_seen[(size_t)at]++ == 0, "C (%lld, %lld) stored twice", (long long)row,
+                      (long long)col);
               }
             }
           }

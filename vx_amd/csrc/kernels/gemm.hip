@@ -204,6 +204,30 @@ __device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
   }
 }
 
+/* Four consecutive elements of C from `at` (one 16-byte store of f32, or
+ * 8 bytes of bf16 / f16, where `vec` says the address allows it). */
+template <int kOut>
+__device__ __forceinline__ void put4(void *c, int64_t at, f32x4 v, bool vec) {
+  if (vec) {
+    if constexpr (kOut == VX_DTYPE_F32) {
+      *reinterpret_cast<f32x4 *>(static_cast<float *>(c) + at) = v;
+    } else {
+      uint32_t h[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        h[r] = kOut == VX_DTYPE_BF16 ? f32_to_bf16(v[r]) : f32_to_f16(v[r]);
+      }
+      *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(c) + at) =
+          uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      put<kOut>(c, at + r, v[r]);
+    }
+  }
+}
+
 template <bool kBf16, int kOut>
 __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
@@ -322,31 +346,36 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     lds_barrier();
     /* compute phase: column blocks outer, row blocks snaking, so the B
      * operand stays put for 8 MFMAs and consecutive MFMAs always share one
-     * operand (fewer operand toggles; about 3% faster at the power limit) */
+     * operand (fewer operand toggles; about 3% faster at the power limit).
+     * B's fragment goes first: the block accumulates C^T, whose lane layout
+     * puts 4 consecutive columns of one C row in each lane (the operands'
+     * lane layouts are the same, so the sums are the same bits). */
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int jj = 0; jj < kTN; ++jj) {
 #pragma unroll
       for (int i0 = 0; i0 < kTM; ++i0) {
         const int i = (jj & 1) ? kTM - 1 - i0 : i0;
-        acc[i][jj] = mfma16<kBf16>(af[i], bfr[jj], acc[i][jj]);
+        acc[i][jj] = mfma16<kBf16>(bfr[jj], af[i], acc[i][jj]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
   }
 
+  /* Each lane stores 4 consecutive columns of a row per block: 32 stores
+   * per wave where 128 scalar ones were. N is a multiple of 8 and the first
+   * column a multiple of 4, so the 4 are all inside C or all past N. */
+  const bool vec = (ldc & 3) == 0 &&
+                   ((uintptr_t)C & (kOut == VX_DTYPE_F32 ? 15 : 7)) == 0;
 #pragma unroll
   for (int i = 0; i < kTM; ++i) {
 #pragma unroll
     for (int jj = 0; jj < kTN; ++jj) {
-      const int64_t col = n0 + pp::c_col(wn, jj, l16);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + pp::c_row(wm, i, r, kc);
-        if (row < M && col < N) {
-          put<kOut>(C, row * ldc + col, acc[i][jj][r]);
-        }
+      const int64_t row = m0 + pp::c_row(wm, i, l16);
+      const int64_t col = n0 + pp::c_col(wn, jj, kc);
+      if (row < M && col < N) {
+        put4<kOut>(C, row * ldc + col, acc[i][jj], vec);
       }
     }
   }

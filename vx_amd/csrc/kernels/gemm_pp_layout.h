@@ -150,10 +150,13 @@ VX_PP_FN int lds_b_read(int wn, int j, int h, int l16, int kc) {
   return k * (kTileN * 2) + pswz_b(k, n >> 3) * 16 + (n & 7) * 2;
 }
 
-/* Row and column within the tile of the C element that accumulator element
- * r of block (i, jj) of wave (wm, wn) holds for the lane (l16, kc). */
-VX_PP_FN int c_row(int wm, int i, int r, int kc) { return wm * 128 + i * 16 + 4 * kc + r; }
-VX_PP_FN int c_col(int wn, int jj, int l16) { return wn * 64 + jj * 16 + l16; }
+/* Row and first column within the tile of the C elements that block
+ * (i, jj) of wave (wm, wn) holds for the lane (l16, kc). The MFMA takes B's
+ * fragment as its first operand and A's as its second, so it accumulates
+ * C^T: the lane's accumulator elements r = 0..3 are columns c_col + r of
+ * row c_row (one 16-byte store of f32). */
+VX_PP_FN int c_row(int wm, int i, int l16) { return wm * 128 + i * 16 + l16; }
+VX_PP_FN int c_col(int wn, int jj, int kc) { return wn * 64 + jj * 16 + 4 * kc; }
 
 } // namespace pp
 } // namespace vxk
