@@ -331,30 +331,36 @@ def test_mfma_pp_against_oracle(hiplib, k, out_dt, rng):
 @pytest.mark.parametrize("m,n,k,ldb", [(1000, 776, 512, 776), (300, 4104, 64, 4104),
                                        (257, 776, 96, 784), (1, 8, 32, 8), (4100, 296, 128, 304)])
 @pytest.mark.parametrize("out_dt", [abi.DTYPE_F32, abi.DTYPE_BF16])
-def test_mfma_pp_ragged_edges(hiplib, m, n, k, ldb, out_dt, rng):
+@pytest.mark.parametrize("pad,col0", [(3, 1), (8, 4)])
+def test_mfma_pp_ragged_edges(hiplib, m, n, k, ldb, out_dt, pad, col0, rng):
     """M and N that are not multiples of the 256x256 tile, and a B whose rows
     are padded (ldb > n): edge tiles read zeros past the operands' ends and
-    store only inside C, which is checked to be untouched around the result."""
-    announce(f"gemm ping-pong ragged {m}x{n}x{k} ldb={ldb} out={out_dt}")
+    store only inside C, which is checked to be untouched around the result.
+    C is a view with row stride n + pad starting at column col0 of row 1:
+    pad 3 puts its rows off the 4-element grid (the epilogue's element
+    stores), pad 8 with col0 4 keeps them on it (its 16-byte f32 and 8-byte
+    bf16 stores of 4 columns)."""
+    announce(f"gemm ping-pong ragged {m}x{n}x{k} ldb={ldb} out={out_dt} pad={pad}")
     a16 = f32_to_bf16(rng.normal(0, 1, (m, k)).astype(np.float32))
     bpad = f32_to_bf16(rng.normal(0, 1, (k, ldb)).astype(np.float32))
     b16 = np.ascontiguousarray(bpad[:, :n])
     da, db = DeviceArray.of(hiplib, a16, abi.DTYPE_BF16), DeviceArray.of(hiplib, bpad, abi.DTYPE_BF16)
     npt = np.float32 if out_dt == abi.DTYPE_F32 else np.uint16
-    sentinel = np.full((m + 2, n + 3), 7, npt)  # C is rows 1..m, cols 1..n of this
+    ldc = n + pad
+    sentinel = np.full((m + 2, ldc), 7, npt)  # C is rows 1..m, cols col0..col0+n-1
     dc = DeviceArray.of(hiplib, sentinel, out_dt)
     hiplib.force_gemm_kernel(abi.GEMM_MFMA_PP)
     before = hiplib.stats()
     matmul(hiplib, da.descriptor(), abi.DTYPE_BF16,
            db.descriptor(sizes=(k, n), strides=(ldb, 1)), abi.DTYPE_BF16,
-           dc.descriptor(sizes=(m, n), strides=(n + 3, 1), offset=n + 3 + 1), out_dt)
+           dc.descriptor(sizes=(m, n), strides=(ldc, 1), offset=ldc + col0), out_dt)
     full = dc.numpy()
     after = hiplib.stats()
     hiplib.force_gemm_kernel(abi.GEMM_AUTO)
     assert after["gemm_mfma"] == before["gemm_mfma"] + 1
-    c = full[1:m + 1, 1:n + 1]
+    c = full[1:m + 1, col0:col0 + n]
     rest = full.copy()
-    rest[1:m + 1, 1:n + 1] = 7
+    rest[1:m + 1, col0:col0 + n] = 7
     assert np.all(rest == 7)
     want = oracle.gemm_bf16_f32(a16, b16)
     if out_dt == abi.DTYPE_F32:
