@@ -251,6 +251,13 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
   const bool live = r0 < a.rows;
   constexpr bool kRes = kMode == kResid || kMode == kAttnResid;
   constexpr bool kQkvLike = kMode == kQkv || kMode == kEmbed;
+  /* The modes whose input is a row vector read as it is (normalised or
+   * not): each lane loads the 16 columns per segment that its weights
+   * multiply, and a wave, whose lanes hold every column, reduces the norm's
+   * sum of squares by itself. No wave waits at a workgroup barrier for
+   * another wave's loads, and the input makes no LDS round trip. */
+  constexpr bool kWaveIn =
+      kMode == kQkv || kMode == kSwiglu || kMode == kLogits || kMode == kResid;
 
   /* Every load is a buffer load whose offset points past its range where
    * the element does not exist (zeros come back), so no branch surrounds a
@@ -301,7 +308,33 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
           __builtin_amdgcn_raw_buffer_load_b32(cr, (int)(ok ? off + 8 : kOut), 0, 0));
     }
   }
-  if constexpr (kMode == kAttnResid) {
+  /* kWaveIn: this lane's input columns s * 1024 + 16 lane .. + 15 (all
+   * inside or all past cols, a multiple of 16), four floats per load. */
+  u32x4 xw[kWaveIn ? kSegs : 1][4], nw[kWaveIn && !kRes ? kSegs : 1][4];
+  if constexpr (kWaveIn) {
+#pragma unroll
+    for (int s = 0; s < kSegs; ++s) {
+      const int c = s * 1024 + lane * 16;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        xw[s][q] = __builtin_amdgcn_raw_buffer_load_b128(
+            xr, (int)(c < cols ? (uint32_t)((c + 4 * q) * 4) : kOut), 0, 0);
+      }
+    }
+    if constexpr (!kRes) {
+      const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
+          (void *)a.norm, (short)0, cols * 4, 0x00020000);
+#pragma unroll
+      for (int s = 0; s < kSegs; ++s) {
+        const int c = s * 1024 + lane * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          nw[s][q] = __builtin_amdgcn_raw_buffer_load_b128(
+              nr, (int)(c < cols ? (uint32_t)((c + 4 * q) * 4) : kOut), 0, 0);
+        }
+      }
+    }
+  } else if constexpr (kMode == kAttnResid) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int i = t + k * kThreads;
@@ -318,15 +351,8 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
             xr, (int)(ok ? mo + 16 * q : kOut), 0, 0);
       }
     }
-  } else if constexpr (kMode != kEmbed) {
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
-      xv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-          xr, (int)(i < cols ? (uint32_t)(i * 4) : kOut), 0, 0));
-    }
   }
-  if constexpr (!kRes) {
+  if constexpr (kMode == kEmbed) {
     const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)a.norm, (short)0, cols * 4, 0x00020000);
 #pragma unroll
@@ -408,12 +434,43 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
           ropr, (int)(mine ? (uint32_t)((row0 + t) * 4) : kOut), 0, 0));
     }
   }
-  if constexpr (kMode == kResid) {
+  /* kWaveIn: the input of this lane's columns, normalised for the norm
+   * modes. */
+  float xn[kWaveIn ? kSegs : 1][16];
+  if constexpr (kWaveIn) {
+    if constexpr (kMode == kQkv) {
+      pos = *a.pos; /* where k and v go in the cache */
+    }
+    if constexpr (kRes) {
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
-      if (i < cols) {
-        xin[i] = xv[k];
+      for (int s = 0; s < kSegs; ++s) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          xn[s][k] = __uint_as_float(xw[s][k >> 2][k & 3]);
+        }
+      }
+    } else {
+      /* RMSNorm as reference examples/llama.vx:145-158. */
+      float ss = 0.0f;
+#pragma unroll
+      for (int s = 0; s < kSegs; ++s) {
+        if (s * 1024 + lane * 16 < cols) {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const float v = __uint_as_float(xw[s][k >> 2][k & 3]);
+            ss += v * v;
+          }
+        }
+      }
+      ss = wave_sum(ss);
+      const float inv = 1.0f / sqrtf(ss / (float)cols + 0.00001f);
+#pragma unroll
+      for (int s = 0; s < kSegs; ++s) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          xn[s][k] = __uint_as_float(nw[s][k >> 2][k & 3]) *
+                     (inv * __uint_as_float(xw[s][k >> 2][k & 3]));
+        }
       }
     }
   } else if constexpr (kMode == kAttnResid) {
@@ -446,7 +503,8 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       xin[i] = num / den;
     }
   } else {
-    if constexpr (kMode == kEmbed) {
+    static_assert(kMode == kEmbed, "the other modes take kWaveIn");
+    {
       /* This position's token: the merge of the candidates (every thread
        * ends with the same Best: the waves exchange theirs through LDS and
        * each thread merges them in the same order). */
@@ -510,9 +568,6 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       }
     }
     /* RMSNorm as reference examples/llama.vx:145-158. */
-    if constexpr (kMode == kQkv) {
-      pos = *a.pos; /* where k and v go in the cache */
-    }
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
@@ -530,7 +585,9 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       }
     }
   }
-  __syncthreads();
+  if constexpr (!kWaveIn) {
+    __syncthreads();
+  }
 
   float acc0 = 0.0f, acc1 = 0.0f;
   Best best{-INFINITY, 0x7fffffff, -INFINITY};
@@ -544,7 +601,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       if (c < cols) {
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-          const float xv = xin[c + k];
+          const float xv = kWaveIn ? xn[s][k] : xin[c + k];
           const float w0 = (float)(int8_t)(wp[p][s][k >> 2] >> (8 * (k & 3)));
           const float w1 = (float)(int8_t)(wq[p][s][k >> 2] >> (8 * (k & 3)));
 #if VX_DEC_DOT_FMA
