@@ -11,9 +11,10 @@ The same JSON line carries:
     (hipEvents on the launch stream over the timed region) against the
     MI355X dense bf16 MFMA peak, and its HBM traffic per launch from the
     committed rocprofv3 PMC summary when one exists;
-  - cpu_baseline: the CPU oracle's bf16 -> f32 GEMM (the reference's
-    outlined-loop semantics, one thread) timed on a bounded block of rows of
-    the same GEMM;
+  - cpu_baseline: the reference's CPU path for the same GEMM, one thread,
+    timed on a bounded block of rows: its x86 dispatch library built here
+    from its sources (oracle/_ref, kind "reference"), or where that was not
+    built the CPU oracle's restatement of it (kind "port");
   - extra: flash-attention forward (config 3), int8 GEMV (config 5, weights
     rotated through more than the 256 MB MALL), int8 greedy decode
     (config 4), the 8192^3 GEMM roofline point and the f32 512^3 plumbing
@@ -470,6 +471,46 @@ def bench_gemv(lib, timer, steps: int, warmup: int):
     return out
 
 
+def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
+    """The reference's own CPU path on a block of rows of the same 4096^3
+    GEMM: its x86 dispatch library (reference runtime/x86_dispatch.cpp, built
+    from its sources into oracle/_ref by oracle/Makefile) driven through the
+    plugin ABI as a compiled `c = a @ b` drives it, on the bf16 operands
+    extended to f32 (the arithmetic of its bf16 -> f32 route: extend, f32
+    multiply-add in k order; tests/test_oracle.py pins the two bit-equal).
+    One thread: the reference's matmul route runs on the dispatching thread
+    (reference runtime/host_dispatch_common.h:616-623)."""
+    import oracle
+    from vx_amd import abi
+    from vx_amd.abi import bf16_to_f32
+    from vx_amd.runtime import matmul
+
+    lib = oracle.ref_lib()
+    a = np.ascontiguousarray(bf16_to_f32(a16), np.float32)
+    b = np.ascontiguousarray(bf16_to_f32(b16), np.float32)
+    n, k = a.shape
+    bd = abi.Descriptor(b.ctypes.data, b.shape)
+
+    def run(rows: int) -> float:
+        c = np.empty((rows, b.shape[1]), np.float32)
+        t0 = time.perf_counter()
+        matmul(lib, abi.Descriptor(a.ctypes.data, (rows, k)), abi.DTYPE_F32, bd, abi.DTYPE_F32,
+               abi.Descriptor(c.ctypes.data, c.shape), abi.DTYPE_F32, outkind="buffer",
+               topo=abi.TOPO_CPU)
+        dt = time.perf_counter() - t0
+        assert np.isfinite(c).all()
+        return dt
+
+    per_row = run(2) / 2
+    rows = int(max(2, min(n, budget_s / max(per_row, 1e-6))))
+    dt = run(rows)
+    flops = 2.0 * rows * k * b.shape[1]
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="reference",
+                sample=f"rows 0..{rows} of the {n}^3 GEMM ({flops / 1e9:.1f} GFLOP in {dt:.1f} s) "
+                       f"through the reference x86 dispatch library (oracle/_ref), f32 on the "
+                       f"bf16 operands extended, 1 thread")
+
+
 def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
     """The CPU oracle's bf16 -> f32 GEMM (one thread) on a block of rows of
     the same 4096^3 GEMM, sized to about `budget_s` of work."""
@@ -683,7 +724,14 @@ def main() -> int:
     cpu = None
     if not ns.skip_cpu:
         log("cpu baseline")
-        cpu = cpu_baseline_gemm(g["a16"], g["b16"])
+        import oracle
+
+        # the reference's own CPU path where its library was built here
+        # (oracle/_ref), else the restatement (oracle/vx_oracle.c)
+        if oracle.ref_available():
+            cpu = cpu_baseline_ref_gemm(g["a16"], g["b16"])
+        else:
+            cpu = cpu_baseline_gemm(g["a16"], g["b16"])
         cpu["nproc"] = os.cpu_count()
         if "flash_attn_fwd" in extra:
             extra["flash_attn_fwd"]["cpu"] = cpu_fa()
