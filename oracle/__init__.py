@@ -222,4 +222,6 @@ def ref_lib():
     """The reference x86 dispatch library (built from the reference sources)
     bound with the plugin ABI signatures."""
     from vx_amd.runtime import DispatchLibrary
-    return DispatchLibrary(REF_LIB, hip=False)
+    # local scope: loaded beside this build's library, it must not supply the
+    # vx_* symbols that outlined host kernels resolve in the global scope
+    return DispatchLibrary(REF_LIB, hip=False, global_scope=False)

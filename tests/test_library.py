@@ -4,8 +4,10 @@ way the reference libraries do without a device: host memory for
 transfers, the outlined host kernel for a dispatch, errors for the ops."""
 
 import ctypes
+import os
 import re
 import subprocess
+import sys
 from pathlib import Path
 
 import numpy as np
@@ -185,6 +187,37 @@ def test_split_regions_run_on_host_workers(cpulib, outlined, monkeypatch, thread
     assert np.all(out[:, 1] == want), out
     assert np.array_equal(out[:, 0], np.arange(12) % want), out
     assert cpulib.lib.vx_host_worker_id() == 0 and cpulib.lib.vx_host_worker_count() == 1
+
+
+def test_reference_library_loaded_first_supplies_no_symbols(cpulib, outlined):
+    """The reference library loaded into the same process before this one (as
+    the oracle's checker or the bench's CPU baseline may load it) stays out of
+    the global symbol scope: an outlined kernel's vx_host_worker_id / _count
+    still resolve to this library and see its worker split. A fresh process,
+    so that the load order is the one under test."""
+    import oracle
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built")
+    script = f"""
+import ctypes, sys
+import numpy as np
+sys.path.insert(0, {str(ROOT)!r})
+import oracle
+from vx_amd import abi
+from vx_amd.runtime import DispatchLibrary
+ref = oracle.ref_lib()
+lib = DispatchLibrary()
+ctypes.CDLL({outlined._name!r}, mode=ctypes.RTLD_GLOBAL)
+out = np.full((12, 2), -1, np.float32)
+args = abi.CallArgs()
+args.memref(abi.Descriptor(out.ctypes.data, out.shape), abi.DTYPE_F32)
+lib.dispatch(abi.payload("vx_test_kernel_2", abi="1", launch="12"), args)
+print(" ".join(str(int(v)) for v in out[:, 1]))
+"""
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True,
+                         timeout=120, env={**os.environ, "VX_HOST_THREADS": "3"})
+    assert res.returncode == 0, res.stderr
+    assert res.stdout.split() == ["3"] * 12, res.stdout
 
 
 def test_matmul_without_a_gpu_runs_the_outlined_loop(cpulib, outlined):

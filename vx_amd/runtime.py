@@ -87,13 +87,20 @@ def bind(lib: ctypes.CDLL, table: dict) -> None:
 class DispatchLibrary:
     """A loaded dispatch library and the ABI calls on it."""
 
-    def __init__(self, path: os.PathLike | str = LIB_PATH, hip: bool = True):
+    def __init__(self, path: os.PathLike | str = LIB_PATH, hip: bool = True,
+                 global_scope: bool = True):
+        """global_scope: load the library into the process's global symbol
+        scope, as a program's one dispatch library is, so outlined host
+        kernels resolve vx_host_worker_id / _count to it. A second dispatch
+        library in the same process (the reference's, as a checker) loads
+        with global_scope=False, so it never supplies those symbols."""
         path = Path(path)
         if not path.exists():
             raise FileNotFoundError(
                 f"{path} is not built; run `python -m vx_amd.build` (or __graft_entry__.build())")
         self.path = path
-        self.lib = ctypes.CDLL(str(path), mode=ctypes.RTLD_GLOBAL)
+        self.lib = ctypes.CDLL(str(path),
+                               mode=ctypes.RTLD_GLOBAL if global_scope else ctypes.RTLD_LOCAL)
         bind(self.lib, SIGNATURES)
         self.hip = hip
         if hip:
