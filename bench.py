@@ -472,8 +472,8 @@ def bench_gemv(lib, timer, steps: int, warmup: int):
 
 
 def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
-    """The reference's own CPU path on a block of rows of the same 4096^3
-    GEMM: its x86 dispatch library (reference runtime/x86_dispatch.cpp, built
+    """The reference's own CPU path on a block of rows of the same GEMM
+    (the headline 4096^3 one, and the 8192^3 one in extra): its x86 dispatch library (reference runtime/x86_dispatch.cpp, built
     from its sources into oracle/_ref by oracle/Makefile) driven through the
     plugin ABI as a compiled `c = a @ b` drives it, on the bf16 operands
     extended to f32 (the arithmetic of its bf16 -> f32 route: extend, f32
@@ -513,7 +513,7 @@ def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
 
 def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
     """The CPU oracle's bf16 -> f32 GEMM (one thread) on a block of rows of
-    the same 4096^3 GEMM, sized to about `budget_s` of work."""
+    the same GEMM, sized to about `budget_s` of work."""
     import oracle
 
     n = a16.shape[0]
@@ -733,6 +733,10 @@ def main() -> int:
         else:
             cpu = cpu_baseline_gemm(g["a16"], g["b16"])
         cpu["nproc"] = os.cpu_count()
+        if "gemm_bf16_8192" in extra:
+            # the same CPU path on a timed block of rows of the 8192^3 GEMM
+            cpu8 = cpu_baseline_ref_gemm if oracle.ref_available() else cpu_baseline_gemm
+            extra["gemm_bf16_8192"]["cpu"] = cpu8(g8["a16"], g8["b16"], budget_s=3.0)
         if "flash_attn_fwd" in extra:
             extra["flash_attn_fwd"]["cpu"] = cpu_fa()
         if "gemv_i8" in extra:
