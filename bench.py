@@ -196,6 +196,7 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
     ms_step = ms_events / steps
     return dict(n=n, m=m, k=k, ms_per_step=ms_step, wall_ms_per_step=wall * 1e3 / (steps * runs),
                 tflops=flops / (ms_step * 1e-3) / 1e12, flops=flops, a16=a16, b16=b16,
+                c_head=np.ascontiguousarray(c[:64]),
                 runs_us=spread([x * 1e3 / steps for x in region_ms]),
                 tflops_runs=spread([flops / (x / steps * 1e-3) / 1e12 for x in region_ms]),
                 steps_us=spread([x * 1e3 for x in step_ms]), clock_mhz=clock_mhz)
@@ -471,7 +472,7 @@ def bench_gemv(lib, timer, steps: int, warmup: int):
     return out
 
 
-def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
+def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0, gpu_rows=None):
     """The reference's own CPU path on a block of rows of the same GEMM
     (the headline 4096^3 one, and the 8192^3 one in extra): its x86 dispatch library (reference runtime/x86_dispatch.cpp, built
     from its sources into oracle/_ref by oracle/Makefile) driven through the
@@ -479,7 +480,8 @@ def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
     extended to f32 (the arithmetic of its bf16 -> f32 route: extend, f32
     multiply-add in k order; tests/test_oracle.py pins the two bit-equal).
     One thread: the reference's matmul route runs on the dispatching thread
-    (reference runtime/host_dispatch_common.h:616-623)."""
+    (reference runtime/host_dispatch_common.h:616-623). With `gpu_rows`
+    (the first rows of the GPU's C), the rows both computed are compared."""
     import oracle
     from vx_amd import abi
     from vx_amd.abi import bf16_to_f32
@@ -491,7 +493,7 @@ def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
     n, k = a.shape
     bd = abi.Descriptor(b.ctypes.data, b.shape)
 
-    def run(rows: int) -> float:
+    def run(rows: int):
         c = np.empty((rows, b.shape[1]), np.float32)
         t0 = time.perf_counter()
         matmul(lib, abi.Descriptor(a.ctypes.data, (rows, k)), abi.DTYPE_F32, bd, abi.DTYPE_F32,
@@ -499,35 +501,50 @@ def cpu_baseline_ref_gemm(a16, b16, budget_s: float = 10.0):
                topo=abi.TOPO_CPU)
         dt = time.perf_counter() - t0
         assert np.isfinite(c).all()
-        return dt
+        return dt, c
 
-    per_row = run(2) / 2
+    per_row = run(2)[0] / 2
     rows = int(max(2, min(n, budget_s / max(per_row, 1e-6))))
-    dt = run(rows)
+    dt, c = run(rows)
     flops = 2.0 * rows * k * b.shape[1]
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="reference",
-                sample=f"rows 0..{rows} of the {n}^3 GEMM ({flops / 1e9:.1f} GFLOP in {dt:.1f} s) "
-                       f"through the reference x86 dispatch library (oracle/_ref), f32 on the "
-                       f"bf16 operands extended, 1 thread")
+    out = dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="reference",
+               sample=f"rows 0..{rows} of the {n}x{b.shape[1]}x{k} GEMM ({flops / 1e9:.1f} GFLOP "
+                      f"in {dt:.1f} s) through the reference x86 dispatch library (oracle/_ref), "
+                      f"f32 on the bf16 operands extended, 1 thread")
+    return _rows_vs_gpu(out, c, gpu_rows)
 
 
-def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0):
+def _rows_vs_gpu(out: dict, cpu_rows, gpu_rows) -> dict:
+    """Adds the comparison of the CPU leg's rows with the GPU's first rows
+    of the same C (the largest absolute difference, against the 1e-4 the
+    GEMM parity tests hold)."""
+    if gpu_rows is not None:
+        r = min(len(cpu_rows), len(gpu_rows))
+        d = float(np.abs(cpu_rows[:r].astype(np.float64) - gpu_rows[:r]).max())
+        out["rows_vs_gpu"] = dict(rows=r, max_abs_diff=d, bound=1e-4, within=d <= 1e-4)
+    return out
+
+
+def cpu_baseline_gemm(a16, b16, budget_s: float = 10.0, gpu_rows=None):
     """The CPU oracle's bf16 -> f32 GEMM (one thread) on a block of rows of
-    the same GEMM, sized to about `budget_s` of work."""
+    the same GEMM, sized to about `budget_s` of work; with `gpu_rows`, its
+    rows compared with the GPU's."""
     import oracle
 
-    n = a16.shape[0]
+    m, k = a16.shape
+    n = b16.shape[1]
     t0 = time.perf_counter()
     oracle.gemm_bf16_f32(a16, b16, rows=slice(0, 2))
     per_row = (time.perf_counter() - t0) / 2
-    rows = int(max(2, min(n, budget_s / max(per_row, 1e-6))))
+    rows = int(max(2, min(m, budget_s / max(per_row, 1e-6))))
     t0 = time.perf_counter()
-    oracle.gemm_bf16_f32(a16, b16, rows=slice(0, rows))
+    c = oracle.gemm_bf16_f32(a16, b16, rows=slice(0, rows))
     dt = time.perf_counter() - t0
-    flops = 2.0 * rows * n * n
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="port",
-                sample=f"rows 0..{rows} of the {n}^3 bf16->f32 GEMM ({flops / 1e9:.1f} GFLOP in "
-                       f"{dt:.1f} s), oracle/vx_oracle.c loop nest, 1 thread")
+    flops = 2.0 * rows * k * n
+    out = dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=1, kind="port",
+               sample=f"rows 0..{rows} of the {m}x{n}x{k} bf16->f32 GEMM ({flops / 1e9:.1f} GFLOP "
+                      f"in {dt:.1f} s), oracle/vx_oracle.c loop nest, 1 thread")
+    return _rows_vs_gpu(out, c[:rows], gpu_rows)
 
 
 def read_ceiling(lib, timer, sizes) -> dict:
@@ -729,14 +746,15 @@ def main() -> int:
         # the reference's own CPU path where its library was built here
         # (oracle/_ref), else the restatement (oracle/vx_oracle.c)
         if oracle.ref_available():
-            cpu = cpu_baseline_ref_gemm(g["a16"], g["b16"])
+            cpu = cpu_baseline_ref_gemm(g["a16"], g["b16"], gpu_rows=g["c_head"])
         else:
-            cpu = cpu_baseline_gemm(g["a16"], g["b16"])
+            cpu = cpu_baseline_gemm(g["a16"], g["b16"], gpu_rows=g["c_head"])
         cpu["nproc"] = os.cpu_count()
         if "gemm_bf16_8192" in extra:
             # the same CPU path on a timed block of rows of the 8192^3 GEMM
             cpu8 = cpu_baseline_ref_gemm if oracle.ref_available() else cpu_baseline_gemm
-            extra["gemm_bf16_8192"]["cpu"] = cpu8(g8["a16"], g8["b16"], budget_s=3.0)
+            extra["gemm_bf16_8192"]["cpu"] = cpu8(g8["a16"], g8["b16"], budget_s=3.0,
+                                                  gpu_rows=g8["c_head"])
         if "flash_attn_fwd" in extra:
             extra["flash_attn_fwd"]["cpu"] = cpu_fa()
         if "gemv_i8" in extra:

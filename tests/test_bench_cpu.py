@@ -54,14 +54,24 @@ def test_reference_cpu_baseline_leg():
     rng = np.random.default_rng(0)
     a16 = f32_to_bf16(rng.normal(0, 1 / 8, (64, 64)).astype(np.float32))
     b16 = f32_to_bf16(rng.normal(0, 1 / 8, (64, 64)).astype(np.float32))
-    r = bench.cpu_baseline_ref_gemm(a16, b16, budget_s=0.05)
+    want = oracle.gemm_bf16_f32(a16, b16)
+    r = bench.cpu_baseline_ref_gemm(a16, b16, budget_s=0.05, gpu_rows=want[:8])
     assert r["kind"] == "reference" and r["cores"] == 1 and r["unit"] == "TFLOP/s"
     assert r["value"] > 0 and "oracle/_ref" in r["sample"]
+    assert r["rows_vs_gpu"]["rows"] == 8 and r["rows_vs_gpu"]["within"]
+    off = want[:8].copy()
+    off[7, 63] += 2e-4  # a wrong element in the last compared row is seen
+    r = bench.cpu_baseline_ref_gemm(a16, b16, budget_s=0.05, gpu_rows=off)
+    assert not r["rows_vs_gpu"]["within"] and r["rows_vs_gpu"]["max_abs_diff"] >= 1.9e-4
 
 
 def test_port_cpu_baseline_leg():
     rng = np.random.default_rng(0)
     a16 = f32_to_bf16(rng.normal(0, 1 / 8, (64, 64)).astype(np.float32))
     b16 = f32_to_bf16(rng.normal(0, 1 / 8, (64, 64)).astype(np.float32))
-    r = bench.cpu_baseline_gemm(a16, b16, budget_s=0.05)
+    want = oracle.gemm_bf16_f32(a16, b16)
+    r = bench.cpu_baseline_gemm(a16[:, :32], b16[:32], budget_s=0.05, gpu_rows=None)
     assert r["kind"] == "port" and r["cores"] == 1 and r["value"] > 0
+    assert "64x64x32" in r["sample"] and "rows_vs_gpu" not in r
+    r = bench.cpu_baseline_gemm(a16, b16, budget_s=0.05, gpu_rows=want[:64])
+    assert r["rows_vs_gpu"]["within"] and r["rows_vs_gpu"]["max_abs_diff"] == 0.0
