@@ -31,8 +31,9 @@
  *
  * Every GEMV is weight-only int8 with one f32 scale per row over f32
  * activations (as in the reference, which is f32 throughout), f32 sums;
- * each wave owns two adjacent rows, so the even/odd RoPE
- * pair and the (h1, h3) SwiGLU pair finish in one lane. Contraction is off
+ * each wave owns pairs of adjacent rows (one pair, two for [W1; W3], four
+ * for the classifier), so the even/odd RoPE pair and the (h1, h3) SwiGLU
+ * pair finish in one lane. Contraction is off
  * so the elementwise arithmetic rounds where the reference's f32 loop nest
  * rounds; the GEMV dot products, whose summation order differs from the
  * reference's anyway, use fused multiply-adds.
@@ -204,14 +205,20 @@ enum Mode { kQkv = 0, kResid = 1, kSwiglu = 2, kLogits = 3, kAttnResid = 4, kEmb
  * candidate); any further ones are read after them. */
 constexpr int kEmbedCand = 4;
 
-/* Row pairs per wave: the classifier's waves take several, so its
- * thousands of rows need fewer workgroups (one round over the CUs). */
 /* Cache policy of the weight loads (0: default; 2: non-temporal). */
 #ifndef VX_DEC_W_CPOL
 #define VX_DEC_W_CPOL 0
 #endif
+/* Row pairs per wave: the classifier's waves take several, so its
+ * thousands of rows need fewer workgroups (one round over the CUs); the
+ * [W1; W3] GEMV's take two, so half as many waves each load and normalise
+ * the input row for the same weights (config 4, graph mode, two rounds:
+ * 1 pair 4867-4871 tok/s, 2 pairs 4946-4951, 4 pairs 4773-4774). */
 #ifndef VX_DEC_LOGIT_PAIRS
 #define VX_DEC_LOGIT_PAIRS 4
+#endif
+#ifndef VX_DEC_SWIGLU_PAIRS
+#define VX_DEC_SWIGLU_PAIRS 2
 #endif
 /* Key and value rows each lane of step_attention_rows requests per round
  * (two rounds in flight). Measured at config 4, graph mode: 4 and 2 about
@@ -230,7 +237,19 @@ constexpr int kEmbedCand = 4;
 #define VX_DEC_DOT_FMA 1
 #endif
 template <int kMode> constexpr int pairs_per_wave() {
-  return kMode == 3 ? VX_DEC_LOGIT_PAIRS : 1;
+  return kMode == kLogits ? VX_DEC_LOGIT_PAIRS : kMode == kSwiglu ? VX_DEC_SWIGLU_PAIRS : 1;
+}
+
+/* SwiGLU of the row pair r, r + 1 of [W1; W3] (rows interleaved: 2i is W1
+ * row i, 2i + 1 is W3 row i; reference :377-384: val * (1 / (1 + exp(-val)))
+ * * h3). */
+__device__ __forceinline__ void swiglu_out(const StepGemvArgs &a, int r, float y0, float y1) {
+#pragma clang fp contract(off)
+  float val = y0;
+  const float neg = 0.0f - val;
+  val = val * (1.0f / (1.0f + expf(neg)));
+  val = val * y1;
+  a.hout[r >> 1] = val;
 }
 
 /* kSegs: 1024-column segments the kernel is built for (cols <= 1024 kSegs),
@@ -627,6 +646,15 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
         best = merge(best, Best{y1, r + 1, -INFINITY});
       }
     }
+    if constexpr (kMode == kSwiglu) {
+      const int r = r0 + 2 * p;
+      if (lane == 0 && r < a.rows) {
+        swiglu_out(a, r, sc0[p] * acc0, sc1[p] * acc1);
+      }
+    }
+  }
+  if constexpr (kMode == kSwiglu) {
+    return; /* each pair stored above */
   }
   if constexpr (kMode == kLogits) {
     /* The next step's position: a vector atomic, nothing waits for it (no
@@ -670,14 +698,6 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
   } else if constexpr (kRes) {
     a.out[r0] = res0 + y0;
     a.out[r0 + 1] = res1 + y1;
-  } else if constexpr (kMode == kSwiglu) {
-    /* rows interleaved: 2i is W1 row i, 2i + 1 is W3 row i (reference
-     * :377-384: val * (1 / (1 + exp(-val))) * h3). */
-    float val = y0;
-    const float neg = 0.0f - val;
-    val = val * (1.0f / (1.0f + expf(neg)));
-    val = val * y1;
-    a.hout[r0 >> 1] = val;
   }
 }
 
