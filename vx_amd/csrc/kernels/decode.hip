@@ -213,7 +213,9 @@ constexpr int kEmbedCand = 4;
  * thousands of rows need fewer workgroups (one round over the CUs); the
  * [W1; W3] GEMV's take two, so half as many waves each load and normalise
  * the input row for the same weights (config 4, graph mode, two rounds:
- * 1 pair 4867-4871 tok/s, 2 pairs 4946-4951, 4 pairs 4773-4774). */
+ * 1 pair 4867-4871 tok/s, 2 pairs 4946-4951, 4 pairs 4773-4774). Two
+ * pairs for the QKV GEMVs measured 4927-4932 against 4939-4953, for W2
+ * (48 workgroups instead of 96) 4825-4828: those keep one. */
 #ifndef VX_DEC_LOGIT_PAIRS
 #define VX_DEC_LOGIT_PAIRS 4
 #endif
@@ -236,20 +238,59 @@ constexpr int kEmbedCand = 4;
 #ifndef VX_DEC_DOT_FMA
 #define VX_DEC_DOT_FMA 1
 #endif
+#ifndef VX_DEC_QKV_PAIRS
+#define VX_DEC_QKV_PAIRS 1
+#endif
+#ifndef VX_DEC_RESID_PAIRS
+#define VX_DEC_RESID_PAIRS 1
+#endif
 template <int kMode> constexpr int pairs_per_wave() {
-  return kMode == kLogits ? VX_DEC_LOGIT_PAIRS : kMode == kSwiglu ? VX_DEC_SWIGLU_PAIRS : 1;
+  return kMode == kLogits   ? VX_DEC_LOGIT_PAIRS
+         : kMode == kSwiglu ? VX_DEC_SWIGLU_PAIRS
+         : kMode == kQkv    ? VX_DEC_QKV_PAIRS
+         : kMode == kResid  ? VX_DEC_RESID_PAIRS
+                            : 1;
 }
 
-/* SwiGLU of the row pair r, r + 1 of [W1; W3] (rows interleaved: 2i is W1
- * row i, 2i + 1 is W3 row i; reference :377-384: val * (1 / (1 + exp(-val)))
- * * h3). */
-__device__ __forceinline__ void swiglu_out(const StepGemvArgs &a, int r, float y0, float y1) {
+/* The results of the row pair r, r + 1 (lane 0 of the wave that owns it;
+ * y0, y1 its scaled sums): q, k (with RoPE) and v at the cache position pos;
+ * the residual adds x += y (res the residual's old values); or SwiGLU. */
+template <int kMode>
+__device__ __forceinline__ void pair_out(const StepGemvArgs &a, int r, int pos, float y0,
+                                         float y1, float fcr, float fci, float res0,
+                                         float res1) {
 #pragma clang fp contract(off)
-  float val = y0;
-  const float neg = 0.0f - val;
-  val = val * (1.0f / (1.0f + expf(neg)));
-  val = val * y1;
-  a.hout[r >> 1] = val;
+  if constexpr (kMode == kQkv || kMode == kEmbed) {
+    const int dim = a.dim, kv_dim = a.kv_dim;
+    if (r < dim + kv_dim) {
+      /* RoPE on the (even, odd) pair (reference :235-264). */
+      const int i = r < dim ? r : r - dim;
+      const float e0 = y0 * fcr - y1 * fci;
+      const float e1 = y0 * fci + y1 * fcr;
+      if (r < dim) {
+        a.out[r] = e0;
+        a.out[r + 1] = e1;
+      } else {
+        a.kcache[(int64_t)pos * kv_dim + i] = e0;
+        a.kcache[(int64_t)pos * kv_dim + i + 1] = e1;
+      }
+    } else {
+      const int i = r - dim - kv_dim;
+      a.vcache[(int64_t)pos * kv_dim + i] = y0;
+      a.vcache[(int64_t)pos * kv_dim + i + 1] = y1;
+    }
+  } else if constexpr (kMode == kResid || kMode == kAttnResid) {
+    a.out[r] = res0 + y0;
+    a.out[r + 1] = res1 + y1;
+  } else if constexpr (kMode == kSwiglu) {
+    /* rows interleaved: 2i is W1 row i, 2i + 1 is W3 row i (reference
+     * :377-384: val * (1 / (1 + exp(-val))) * h3). */
+    float val = y0;
+    const float neg = 0.0f - val;
+    val = val * (1.0f / (1.0f + expf(neg)));
+    val = val * y1;
+    a.hout[r >> 1] = val;
+  }
 }
 
 /* kSegs: 1024-column segments the kernel is built for (cols <= 1024 kSegs),
@@ -267,7 +308,6 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
   const int lane = t & 63;
   const int pair0 = (blockIdx.x * (kThreads / 64) + wave) * kPairs;
   const int r0 = pair0 * 2; /* the first (for kPairs == 1, the only) pair */
-  const bool live = r0 < a.rows;
   constexpr bool kRes = kMode == kResid || kMode == kAttnResid;
   constexpr bool kQkvLike = kMode == kQkv || kMode == kEmbed;
   /* The modes whose input is a row vector read as it is (normalised or
@@ -414,14 +454,24 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
     pos = *a.pos;
     ptok = e.tok.prompt[min(pos, e.tok.n_prompt - 1)]; /* clamped: no branch */
   }
-  float res0 = 0.0f, res1 = 0.0f;
+  float res0[kPairs], res1[kPairs];
+#pragma unroll
+  for (int p = 0; p < kPairs; ++p) {
+    res0[p] = 0.0f;
+    res1[p] = 0.0f;
+  }
   if constexpr (kRes) {
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)a.out, (short)0, a.rows * 4, 0x00020000);
-    res0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        rr, (int)(live ? (uint32_t)(r0 * 4) : kOut), 0, 0));
-    res1 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        rr, (int)(live ? (uint32_t)(r0 * 4 + 4) : kOut), 0, 0));
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+      const int r = r0 + 2 * p;
+      const bool ok = r < a.rows;
+      res0[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          rr, (int)(ok ? (uint32_t)(r * 4) : kOut), 0, 0));
+      res1[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          rr, (int)(ok ? (uint32_t)(r * 4 + 4) : kOut), 0, 0));
+    }
   }
   if constexpr (kMode == kAttnResid) {
     /* Keep the merge's arithmetic behind every load: scheduled earlier, it
@@ -434,19 +484,28 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
    * loaded first, and workgroup 0 also takes the whole row (ropev) to store
    * it for the other layers, whose a.rope then holds it: those request
    * theirs behind the weights without waiting for the position. */
-  float fcr = 0.0f, fci = 0.0f, ropev = 0.0f;
+  float fcr[kPairs], fci[kPairs], ropev = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kPairs; ++p) {
+    fcr[p] = 0.0f;
+    fci[p] = 0.0f;
+  }
   if constexpr (kQkvLike) {
     const bool embed = kMode == kEmbed;
     const int row0 = embed ? pos * a.hs : 0; /* first float of the row */
     const __amdgpu_buffer_rsrc_t ropr = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(embed ? e.rope_table : a.rope), (short)0,
         (embed ? e.seq_len : 1) * a.hs * 4, 0x00020000);
-    const int i = r0 < a.dim ? r0 : r0 - a.dim;
-    const bool rot = live && r0 < a.dim + a.kv_dim;
-    const uint32_t roff = rot ? (uint32_t)((row0 + i % a.hs) * 4) : kOut;
-    fcr = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ropr, (int)roff, 0, 0));
-    fci = __uint_as_float(
-        __builtin_amdgcn_raw_buffer_load_b32(ropr, (int)(rot ? roff + 4 : kOut), 0, 0));
+#pragma unroll
+    for (int p = 0; p < kPairs; ++p) {
+      const int r = r0 + 2 * p;
+      const int i = r < a.dim ? r : r - a.dim;
+      const bool rot = r < a.rows && r < a.dim + a.kv_dim;
+      const uint32_t roff = rot ? (uint32_t)((row0 + i % a.hs) * 4) : kOut;
+      fcr[p] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ropr, (int)roff, 0, 0));
+      fci[p] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(ropr, (int)(rot ? roff + 4 : kOut), 0, 0));
+    }
     if constexpr (embed) {
       const bool mine = blockIdx.x == 0 && t < a.hs;
       ropev = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
@@ -646,15 +705,14 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
         best = merge(best, Best{y1, r + 1, -INFINITY});
       }
     }
-    if constexpr (kMode == kSwiglu) {
+    if constexpr (kMode != kLogits) {
+      /* this pair's results out as its sums land */
       const int r = r0 + 2 * p;
       if (lane == 0 && r < a.rows) {
-        swiglu_out(a, r, sc0[p] * acc0, sc1[p] * acc1);
+        pair_out<kMode>(a, r, pos, sc0[p] * acc0, sc1[p] * acc1, fcr[p], fci[p], res0[p],
+                        res1[p]);
       }
     }
-  }
-  if constexpr (kMode == kSwiglu) {
-    return; /* each pair stored above */
   }
   if constexpr (kMode == kLogits) {
     /* The next step's position: a vector atomic, nothing waits for it (no
@@ -669,35 +727,6 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
     if (blockIdx.x == 0 && t < a.hs) {
       e.rope_out[t] = ropev;
     }
-  }
-  if (lane != 0 || !live) {
-    return;
-  }
-  const float y0 = sc0[0] * acc0;
-  const float y1 = sc1[0] * acc1;
-
-  if constexpr (kQkvLike) {
-    const int dim = a.dim, kv_dim = a.kv_dim;
-    if (r0 < dim + kv_dim) {
-      /* RoPE on the (even, odd) pair (reference :235-264). */
-      const int i = r0 < dim ? r0 : r0 - dim;
-      const float e0 = y0 * fcr - y1 * fci;
-      const float e1 = y0 * fci + y1 * fcr;
-      if (r0 < dim) {
-        a.out[r0] = e0;
-        a.out[r0 + 1] = e1;
-      } else {
-        a.kcache[(int64_t)pos * kv_dim + i] = e0;
-        a.kcache[(int64_t)pos * kv_dim + i + 1] = e1;
-      }
-    } else {
-      const int i = r0 - dim - kv_dim;
-      a.vcache[(int64_t)pos * kv_dim + i] = y0;
-      a.vcache[(int64_t)pos * kv_dim + i + 1] = y1;
-    }
-  } else if constexpr (kRes) {
-    a.out[r0] = res0 + y0;
-    a.out[r0 + 1] = res1 + y1;
   }
 }
 
