@@ -244,6 +244,27 @@ constexpr int kEmbedCand = 4;
 #ifndef VX_DEC_RESID_PAIRS
 #define VX_DEC_RESID_PAIRS 1
 #endif
+/* Waves per workgroup of each GEMV: 4 (256 threads), but 2 for the QKV
+ * GEMVs of layers 1-11 (576 workgroups of one row pair per wave). Config 4,
+ * graph mode, interleaved on one box: QKV 4 / 2 / 1 waves 4928-4932 /
+ * 4961 / 4965-4971 tok/s, and on another box 4 / 2 4994-5001 / 5019-5025;
+ * [W1; W3] 2 / 8 waves 4887-4894 / 4773-4776 against 4994-5001 at 4; W2 and
+ * Wo 2 / 8 waves 4742-4745 / 4787 against 4994-5001 and 4928-4932. */
+#ifndef VX_DEC_QKV_WAVES
+#define VX_DEC_QKV_WAVES 2
+#endif
+#ifndef VX_DEC_SWIGLU_WAVES
+#define VX_DEC_SWIGLU_WAVES 4
+#endif
+#ifndef VX_DEC_RESID_WAVES
+#define VX_DEC_RESID_WAVES 4
+#endif
+template <int kMode> constexpr int group_threads() {
+  return 64 * (kMode == kQkv                                 ? VX_DEC_QKV_WAVES
+               : kMode == kSwiglu                            ? VX_DEC_SWIGLU_WAVES
+               : kMode == kResid || kMode == kAttnResid      ? VX_DEC_RESID_WAVES
+                                                             : 4);
+}
 template <int kMode> constexpr int pairs_per_wave() {
   return kMode == kLogits   ? VX_DEC_LOGIT_PAIRS
          : kMode == kSwiglu ? VX_DEC_SWIGLU_PAIRS
@@ -298,15 +319,16 @@ __device__ __forceinline__ void pair_out(const StepGemvArgs &a, int r, int pos, 
 template <int kMode, int kSegs>
 __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbedArgs &e) {
 #pragma clang fp contract(off)
+  constexpr int kT = group_threads<kMode>(); /* threads per workgroup */
   constexpr int kCols = kSegs * 1024;
   __shared__ float xin[kCols];
-  __shared__ float scratch[kThreads / 64];
+  __shared__ float scratch[kT / 64];
   constexpr int kPairs = pairs_per_wave<kMode>();
   const int t = threadIdx.x;
   const int cols = a.cols;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int pair0 = (blockIdx.x * (kThreads / 64) + wave) * kPairs;
+  const int pair0 = (blockIdx.x * (kT / 64) + wave) * kPairs;
   const int r0 = pair0 * 2; /* the first (for kPairs == 1, the only) pair */
   constexpr bool kRes = kMode == kResid || kMode == kAttnResid;
   constexpr bool kQkvLike = kMode == kQkv || kMode == kEmbed;
@@ -326,7 +348,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
    * runs while the weights stream; then the weights; then the epilogue's
    * operands (row scales; for the residual kernels the residual itself). */
   constexpr uint32_t kOut = 0x80000000u; /* past every range */
-  constexpr int kPer = kCols / kThreads;
+  constexpr int kPer = kCols / kT;
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void *)a.w, (short)0, a.rows * cols, 0x00020000);
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
@@ -357,7 +379,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
         (void *)e.tok.cand, (short)0, ncand * (int)sizeof(Best), 0x00020000);
 #pragma unroll
     for (int c = 0; c < kCand; ++c) {
-      const int j = t + c * kThreads;
+      const int j = t + c * kT;
       const bool ok = j < ncand;
       const uint32_t off = (uint32_t)(j * (int)sizeof(Best));
       cv1[c] = __uint_as_float(
@@ -396,7 +418,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
   } else if constexpr (kMode == kAttnResid) {
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
+      const int i = t + k * kT;
       const bool ok = i < cols;
 #pragma unroll
       for (int p = 0; p < kAttnSplit; ++p) {
@@ -416,7 +438,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
         (void *)a.norm, (short)0, cols * 4, 0x00020000);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
+      const int i = t + k * kT;
       nv[k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
           nr, (int)(i < cols ? (uint32_t)(i * 4) : kOut), 0, 0));
     }
@@ -556,7 +578,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
      * M the largest split max (an empty split has m = -inf, l = o = 0). */
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
+      const int i = t + k * kT;
       float mv[kAttnSplit], lv[kAttnSplit];
 #pragma unroll
       for (int p = 0; p < kAttnSplit; ++p) {
@@ -586,15 +608,15 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       /* This position's token: the merge of the candidates (every thread
        * ends with the same Best: the waves exchange theirs through LDS and
        * each thread merges them in the same order). */
-      __shared__ Best wb[kThreads / 64];
+      __shared__ Best wb[kT / 64];
       Best b{-INFINITY, 0x7fffffff, -INFINITY};
 #pragma unroll
       for (int c = 0; c < kCand; ++c) {
-        const bool ok = t + c * kThreads < e.tok.ncand;
+        const bool ok = t + c * kT < e.tok.ncand;
         b = merge(b, Best{ok ? cv1[c] : -INFINITY, ok ? ci1[c] : 0x7fffffff,
                           ok ? cv2[c] : -INFINITY});
       }
-      for (int j = t + kCand * kThreads; j < e.tok.ncand; j += kThreads) {
+      for (int j = t + kCand * kT; j < e.tok.ncand; j += kT) {
         b = merge(b, e.tok.cand[j]);
       }
       b = best_xchg<1>(b);
@@ -609,7 +631,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       __syncthreads();
       Best r = wb[0];
 #pragma unroll
-      for (int w = 1; w < kThreads / 64; ++w) {
+      for (int w = 1; w < kT / 64; ++w) {
         r = merge(r, wb[w]);
       }
       const bool prompt = pos < e.tok.n_prompt;
@@ -630,7 +652,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       const float es = e.tok.tok_s[tok];
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
-        const int i = t + k * kThreads;
+        const int i = t + k * kT;
         const int8_t e = (int8_t)__builtin_amdgcn_raw_buffer_load_b8(
             er, (int)(i < cols ? (uint32_t)i : kOut), 0, 0);
         xv[k] = (float)e * es;
@@ -638,7 +660,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
       if (blockIdx.x == 0) {
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
-          const int i = t + k * kThreads;
+          const int i = t + k * kT;
           if (i < cols) {
             e.xout[i] = xv[k];
           }
@@ -649,7 +671,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      if (t + k * kThreads < cols) {
+      if (t + k * kT < cols) {
         ss += xv[k] * xv[k];
       }
     }
@@ -657,7 +679,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
     const float inv = 1.0f / sqrtf(ss / (float)cols + 0.00001f);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int i = t + k * kThreads;
+      const int i = t + k * kT;
       if (i < cols) {
         xin[i] = nv[k] * (inv * xv[k]);
       }
@@ -731,7 +753,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
 }
 
 template <int kMode, int kSegs>
-__global__ __launch_bounds__(kThreads) void step_gemv(StepGemvArgs a) {
+__global__ __launch_bounds__(group_threads<kMode>()) void step_gemv(StepGemvArgs a) {
   gemv_body<kMode, kSegs>(a, StepEmbedArgs{});
 }
 
@@ -1203,20 +1225,20 @@ __global__ void step_start(StepArgmaxArgs a) {
 }
 
 template <int kMode> int gemv_groups(int rows) {
-  constexpr int kPerGroup = (kThreads / 64) * pairs_per_wave<kMode>();
+  constexpr int kPerGroup = (group_threads<kMode>() / 64) * pairs_per_wave<kMode>();
   return (rows / 2 + kPerGroup - 1) / kPerGroup;
 }
 
 template <int kMode>
 void launch_gemv(const StepGemvArgs &a, hipStream_t s) {
   const dim3 grid(gemv_groups<kMode>(a.rows));
+  const dim3 block(group_threads<kMode>());
   if (a.cols <= 1024) {
-    hipLaunchKernelGGL((step_gemv<kMode, 1>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((step_gemv<kMode, 1>), grid, block, 0, s, a);
   } else if (a.cols <= 2048) {
-    hipLaunchKernelGGL((step_gemv<kMode, 2>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((step_gemv<kMode, 2>), grid, block, 0, s, a);
   } else {
-    hipLaunchKernelGGL((step_gemv<kMode, kMaxCols / 1024>), grid, dim3(kThreads),
-                       0, s, a);
+    hipLaunchKernelGGL((step_gemv<kMode, kMaxCols / 1024>), grid, block, 0, s, a);
   }
 }
 
