@@ -46,11 +46,13 @@ struct LlamaI8 {
   vxk::StepBest *best = nullptr; /* one per classifier workgroup */
   int prompt_cap = 0, out_cap = 0;
   hipStream_t stream = nullptr;
-  /* The instantiated step graphs (one step, kGraphSteps steps), kept across
-   * generate calls: they bake in the prompt length and the I/O buffers, so
-   * they are dropped when either changes. */
-  hipGraphExec_t step_exec = nullptr;
-  hipGraphExec_t steps_exec = nullptr;
+  /* The instantiated step graphs (one step, kGraphSteps steps; [1]: for
+   * steps whose positions are all below step_attention_near, whose
+   * attention takes smaller rounds of rows), kept across generate calls:
+   * they bake in the prompt length and the I/O buffers, so they are dropped
+   * when either changes. */
+  hipGraphExec_t step_exec[2] = {nullptr, nullptr};
+  hipGraphExec_t steps_exec[2] = {nullptr, nullptr};
   int step_exec_prompt = -1;
   std::vector<void *> owned;
 };
@@ -70,7 +72,8 @@ template <typename T> T *alloc(LlamaI8 &m, size_t count) {
 }
 
 void drop_step_graph(LlamaI8 &m) {
-  for (hipGraphExec_t *g : {&m.step_exec, &m.steps_exec}) {
+  for (hipGraphExec_t *g : {&m.step_exec[0], &m.step_exec[1], &m.steps_exec[0],
+                            &m.steps_exec[1]}) {
     if (*g) {
       (void)hipGraphExecDestroy(*g);
       *g = nullptr;
@@ -133,8 +136,9 @@ vxk::StepArgmaxArgs argmax_args(LlamaI8 &m, int n_prompt) {
   return a;
 }
 
-/* One token step on the model's stream. */
-void enqueue_step(LlamaI8 &m, int n_prompt) {
+/* One token step on the model's stream; `near`: its position is below
+ * step_attention_near (the attention launches take smaller rounds). */
+void enqueue_step(LlamaI8 &m, int n_prompt, bool near) {
   const vx_llama_i8_config &c = m.cfg;
   const int qkv_rows = c.dim + 2 * m.kv_dim;
   const int64_t layer_kv = (int64_t)c.seq_len * m.kv_dim;
@@ -179,7 +183,7 @@ void enqueue_step(LlamaI8 &m, int n_prompt) {
     at.hs = m.hs;
     at.kv_mul = c.n_heads / c.n_kv_heads;
     at.seq_len = c.seq_len;
-    vxk::step_attention_launch(at, c.n_heads, c.seq_len, m.stream);
+    vxk::step_attention_launch(at, c.n_heads, c.seq_len, m.stream, near);
 
     vxk::StepGemvArgs wo = g;
     wo.w = m.wo + (int64_t)l * c.dim * c.dim;
@@ -354,37 +358,39 @@ int32_t vx_llama_i8_generate(void *model, const int32_t *prompt,
   vxk::StepArgmaxArgs start = argmax_args(*m, n_prompt);
   vxk::step_start_launch(start, m->stream);
   const int positions = n_prompt + n_steps - 1;
+  const int near_pos = vxk::step_attention_near(m->hs);
   if (flags & VX_LLAMA_GRAPH) {
-    if (!m->step_exec || m->step_exec_prompt != n_prompt) {
+    if (m->step_exec_prompt != n_prompt) {
       drop_step_graph(*m);
-      auto capture = [&](int steps) {
+      m->step_exec_prompt = n_prompt;
+    }
+    /* the graph of `steps` steps for positions p .. p + steps - 1,
+     * captured when first needed */
+    auto graph_for = [&](int p, int steps) {
+      const int near = p + steps - 1 < near_pos ? 1 : 0;
+      hipGraphExec_t &exec = steps == 1 ? m->step_exec[near] : m->steps_exec[near];
+      if (!exec) {
         hipGraph_t graph = nullptr;
-        hipGraphExec_t exec = nullptr;
         VX_HIP_CHECK(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
         for (int i = 0; i < steps; ++i) {
-          enqueue_step(*m, n_prompt);
+          enqueue_step(*m, n_prompt, near != 0);
         }
         VX_HIP_CHECK(hipStreamEndCapture(m->stream, &graph));
         VX_HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
         VX_HIP_CHECK(hipGraphDestroy(graph));
-        return exec;
-      };
-      m->step_exec = capture(1);
-      if (kGraphSteps > 1) {
-        m->steps_exec = capture(kGraphSteps);
       }
-      m->step_exec_prompt = n_prompt;
-    }
+      return exec;
+    };
     int p = 0;
     for (; kGraphSteps > 1 && p + kGraphSteps <= positions; p += kGraphSteps) {
-      VX_HIP_CHECK(hipGraphLaunch(m->steps_exec, m->stream));
+      VX_HIP_CHECK(hipGraphLaunch(graph_for(p, kGraphSteps), m->stream));
     }
     for (; p < positions; ++p) {
-      VX_HIP_CHECK(hipGraphLaunch(m->step_exec, m->stream));
+      VX_HIP_CHECK(hipGraphLaunch(graph_for(p, 1), m->stream));
     }
   } else {
     for (int p = 0; p < positions; ++p) {
-      enqueue_step(*m, n_prompt);
+      enqueue_step(*m, n_prompt, p < near_pos);
     }
   }
   /* the token after the last step */
@@ -420,8 +426,9 @@ int32_t vx_llama_i8_logits(void *model, const int32_t *tokens, int32_t n,
                               hipMemcpyHostToDevice, m->stream));
   vxk::step_start_launch(argmax_args(*m, n), m->stream);
   const size_t vocab = (size_t)m->cfg.vocab_size;
+  const int near_pos = vxk::step_attention_near(m->hs);
   for (int p = 0; p < n; ++p) {
-    enqueue_step(*m, n);
+    enqueue_step(*m, n, p < near_pos);
     VX_HIP_CHECK(hipMemcpyAsync(logits + p * vocab, m->logits,
                                 sizeof(float) * vocab, hipMemcpyDeviceToHost,
                                 m->stream));

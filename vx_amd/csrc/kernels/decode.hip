@@ -223,12 +223,18 @@ constexpr int kEmbedCand = 4;
 #define VX_DEC_SWIGLU_PAIRS 2
 #endif
 /* Key and value rows each lane of step_attention_rows requests per round
- * (two rounds in flight). Measured at config 4, graph mode: 4 and 2 about
- * 3% faster than 8, whose first round fetches 64 KiB per workgroup before
- * the position is known (four times what the bench's positions need). */
+ * (two rounds in flight): 4, and 2 for launches whose positions the first
+ * two rounds of 2 cover (kNearChunk; the host picks, see
+ * step_attention_near). Smaller rounds make the first round, requested
+ * before the position is known, and each round's arithmetic cheaper; larger
+ * ones need fewer round trips at long caches. Config 4, graph mode: 4 and
+ * 2 about 3% faster than 8 (whose first round fetches 64 KiB per workgroup
+ * before the position is known); 2 at every position 5013-5015 tok/s
+ * against 4949-4952 for 4, and 1 at every position 4964-4968. */
 #ifndef VX_ATTN_CHUNK
 #define VX_ATTN_CHUNK 4
 #endif
+constexpr int kNearChunk = 2;
 /* The GEMVs' dot products with fused multiply-adds (1) or a multiply and an
  * add per term (0). Their summation order differs from the reference's loop
  * in either case; the elementwise arithmetic stays unfused. Fused: one VALU
@@ -1006,13 +1012,12 @@ template <int kL> __device__ __forceinline__ float slot_sum(float v) {
  * repeat with the usual online rescale while positions remain, the next
  * round's rows in flight while one is scored. The four waves' (max, sum,
  * weighted values) then meet once in LDS. */
-template <int kL>
+template <int kL, int kChunk> /* kChunk: rows per lane in flight */
 __global__ __launch_bounds__(kThreads) void step_attention_rows(StepAttnArgs a) {
 #pragma clang fp contract(off)
   constexpr int kE = 4;
   constexpr int hs = kE * kL;
   constexpr int kPerWave = 64 / kL;       /* positions a wave scores at once */
-  constexpr int kChunk = VX_ATTN_CHUNK;   /* rows per lane in flight */
   constexpr int kStride = 4 * kPerWave;   /* local rows between a wave's rows */
   constexpr int kRound = kStride * kChunk; /* local rows per round */
   __shared__ float wo[4][hs];
@@ -1279,8 +1284,17 @@ void step_record_launch(const StepArgmaxArgs &a, hipStream_t s) {
   hipLaunchKernelGGL(step_record, dim3(1), dim3(kChooseThreads), 0, s, a);
 }
 
+template <int kL>
+void launch_rows(const StepAttnArgs &a, dim3 grid, bool near, hipStream_t s) {
+  if (near) {
+    hipLaunchKernelGGL((step_attention_rows<kL, kNearChunk>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((step_attention_rows<kL, VX_ATTN_CHUNK>), grid, dim3(kThreads), 0, s, a);
+  }
+}
+
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
-                           hipStream_t s) {
+                           hipStream_t s, bool near) {
   const size_t lds = (size_t)((seq_len + kAttnSplit - 1) / kAttnSplit) * sizeof(float);
   const dim3 grid(heads, kAttnSplit);
   switch (a.hs) {
@@ -1288,11 +1302,20 @@ void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
   case 4: hipLaunchKernelGGL((step_attention<4, 1>), grid, dim3(kThreads), lds, s, a); break;
   case 8: hipLaunchKernelGGL((step_attention<4, 2>), grid, dim3(kThreads), lds, s, a); break;
   case 16: hipLaunchKernelGGL((step_attention<4, 4>), grid, dim3(kThreads), lds, s, a); break;
-  case 32: hipLaunchKernelGGL((step_attention_rows<8>), grid, dim3(kThreads), 0, s, a); break;
-  case 64: hipLaunchKernelGGL((step_attention_rows<16>), grid, dim3(kThreads), 0, s, a); break;
-  case 128: hipLaunchKernelGGL((step_attention_rows<32>), grid, dim3(kThreads), 0, s, a); break;
-  default: hipLaunchKernelGGL((step_attention_rows<64>), grid, dim3(kThreads), 0, s, a); break;
+  case 32: launch_rows<8>(a, grid, near, s); break;
+  case 64: launch_rows<16>(a, grid, near, s); break;
+  case 128: launch_rows<32>(a, grid, near, s); break;
+  default: launch_rows<64>(a, grid, near, s); break;
   }
+}
+
+int step_attention_near(int hs) {
+  if (hs < 32) {
+    return 0; /* the per-thread kernel has one shape */
+  }
+  /* positions the first two small rounds cover: 2 rounds x (4 waves x
+   * 64 / (hs / 4) positions per wave x kNearChunk) local rows x kAttnSplit */
+  return 2 * 4 * (64 / (hs / 4)) * kNearChunk * kAttnSplit;
 }
 
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s) {

@@ -115,9 +115,13 @@ void step_gemv_logits(const StepGemvArgs &a, hipStream_t s);
 int step_logits_groups(int rows);
 /* Records the token of position *pos (after the last step). */
 void step_record_launch(const StepArgmaxArgs &a, hipStream_t s);
-/* hs divides 256 and is at most 256; seq_len * 4 bytes of LDS. */
+/* hs divides 256 and is at most 256; seq_len * 4 bytes of LDS. `near`:
+ * every position this launch may run at is below step_attention_near(hs),
+ * which takes a variant with smaller rounds of rows (any position gives
+ * the same result either way; only the speed differs). */
 void step_attention_launch(const StepAttnArgs &a, int heads, int seq_len,
-                           hipStream_t s);
+                           hipStream_t s, bool near = false);
+int step_attention_near(int hs);
 /* pos = 0. */
 void step_start_launch(const StepArgmaxArgs &a, hipStream_t s);
 
