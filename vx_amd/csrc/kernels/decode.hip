@@ -180,8 +180,9 @@ template <int kO> __device__ __forceinline__ Best best_xchg(Best b) {
 /* Classifier epilogue: the best and runner-up of this workgroup's rows
  * (each wave's lane 0 holds its own in `b`) into part[blockIdx.x], for the
  * next step's token choice (step_gemv_embed, or step_record) to merge. */
+template <int kWaves>
 __device__ void logits_best(const StepGemvArgs &a, Best b) {
-  __shared__ Best wbest[kThreads / 64];
+  __shared__ Best wbest[kWaves];
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
@@ -191,7 +192,7 @@ __device__ void logits_best(const StepGemvArgs &a, Best b) {
   __syncthreads();
   if (t == 0) {
     Best m = wbest[0];
-    for (int w = 1; w < kThreads / 64; ++w) {
+    for (int w = 1; w < kWaves; ++w) {
       m = merge(m, wbest[w]);
     }
     a.part[blockIdx.x] = m;
@@ -255,7 +256,11 @@ constexpr int kNearChunk = 2;
  * graph mode, interleaved on one box: QKV 4 / 2 / 1 waves 4928-4932 /
  * 4961 / 4965-4971 tok/s, and on another box 4 / 2 4994-5001 / 5019-5025;
  * [W1; W3] 2 / 8 waves 4887-4894 / 4773-4776 against 4994-5001 at 4; W2 and
- * Wo 2 / 8 waves 4742-4745 / 4787 against 4994-5001 and 4928-4932. */
+ * Wo 2 / 8 waves 4742-4745 / 4787 against 4994-5001 and 4928-4932. Then
+ * each alone, against 5055-5056 at 4: Wo 2 / 8 waves 4734-4745 / 5055-5057
+ * (each Wo workgroup merges every column's attention partials, so more
+ * workgroups repeat that work), the classifier 2 / 8 waves 5021-5022 /
+ * 5055-5057, layer 0's QKV 2 waves 5031-5035. */
 #ifndef VX_DEC_QKV_WAVES
 #define VX_DEC_QKV_WAVES 2
 #endif
@@ -265,11 +270,22 @@ constexpr int kNearChunk = 2;
 #ifndef VX_DEC_RESID_WAVES
 #define VX_DEC_RESID_WAVES 4
 #endif
+#ifndef VX_DEC_WO_WAVES
+#define VX_DEC_WO_WAVES 4
+#endif
+#ifndef VX_DEC_LOGIT_WAVES
+#define VX_DEC_LOGIT_WAVES 4
+#endif
+#ifndef VX_DEC_EMBED_WAVES
+#define VX_DEC_EMBED_WAVES 4
+#endif
 template <int kMode> constexpr int group_threads() {
-  return 64 * (kMode == kQkv                                 ? VX_DEC_QKV_WAVES
-               : kMode == kSwiglu                            ? VX_DEC_SWIGLU_WAVES
-               : kMode == kResid || kMode == kAttnResid      ? VX_DEC_RESID_WAVES
-                                                             : 4);
+  return 64 * (kMode == kQkv          ? VX_DEC_QKV_WAVES
+               : kMode == kSwiglu     ? VX_DEC_SWIGLU_WAVES
+               : kMode == kResid      ? VX_DEC_RESID_WAVES
+               : kMode == kAttnResid  ? VX_DEC_WO_WAVES
+               : kMode == kLogits     ? VX_DEC_LOGIT_WAVES
+                                      : VX_DEC_EMBED_WAVES);
 }
 template <int kMode> constexpr int pairs_per_wave() {
   return kMode == kLogits   ? VX_DEC_LOGIT_PAIRS
@@ -748,7 +764,7 @@ __device__ __forceinline__ void gemv_body(const StepGemvArgs &a, const StepEmbed
     if (blockIdx.x == 0 && t == 0) {
       atomicAdd(a.pos, 1);
     }
-    logits_best(a, best);
+    logits_best<kT / 64>(a, best);
     return;
   }
   if constexpr (kMode == kEmbed) {
@@ -764,7 +780,8 @@ __global__ __launch_bounds__(group_threads<kMode>()) void step_gemv(StepGemvArgs
 }
 
 template <int kSegs>
-__global__ __launch_bounds__(kThreads) void step_gemv_embed(StepGemvArgs a, StepEmbedArgs e) {
+__global__ __launch_bounds__(group_threads<kEmbed>()) void step_gemv_embed(StepGemvArgs a,
+                                                                           StepEmbedArgs e) {
   gemv_body<kEmbed, kSegs>(a, e);
 }
 
@@ -1249,13 +1266,13 @@ void launch_gemv(const StepGemvArgs &a, hipStream_t s) {
 
 void launch_embed(const StepGemvArgs &a, const StepEmbedArgs &e, hipStream_t s) {
   const dim3 grid(gemv_groups<kEmbed>(a.rows));
+  const dim3 block(group_threads<kEmbed>());
   if (a.cols <= 1024) {
-    hipLaunchKernelGGL((step_gemv_embed<1>), grid, dim3(kThreads), 0, s, a, e);
+    hipLaunchKernelGGL((step_gemv_embed<1>), grid, block, 0, s, a, e);
   } else if (a.cols <= 2048) {
-    hipLaunchKernelGGL((step_gemv_embed<2>), grid, dim3(kThreads), 0, s, a, e);
+    hipLaunchKernelGGL((step_gemv_embed<2>), grid, block, 0, s, a, e);
   } else {
-    hipLaunchKernelGGL((step_gemv_embed<kMaxCols / 1024>), grid, dim3(kThreads), 0, s,
-                       a, e);
+    hipLaunchKernelGGL((step_gemv_embed<kMaxCols / 1024>), grid, block, 0, s, a, e);
   }
 }
 
