@@ -252,7 +252,8 @@ constexpr int kNearChunk = 2;
 #define VX_DEC_RESID_PAIRS 1
 #endif
 /* Waves per workgroup of each GEMV: 4 (256 threads), but 2 for the QKV
- * GEMVs of layers 1-11 (576 workgroups of one row pair per wave). Config 4,
+ * GEMVs of layers 1-11 (576 workgroups of one row pair per wave) and for
+ * W2. Config 4,
  * graph mode, interleaved on one box: QKV 4 / 2 / 1 waves 4928-4932 /
  * 4961 / 4965-4971 tok/s, and on another box 4 / 2 4994-5001 / 5019-5025;
  * [W1; W3] 2 / 8 waves 4887-4894 / 4773-4776 against 4994-5001 at 4; W2 and
@@ -260,7 +261,9 @@ constexpr int kNearChunk = 2;
  * each alone, against 5055-5056 at 4: Wo 2 / 8 waves 4734-4745 / 5055-5057
  * (each Wo workgroup merges every column's attention partials, so more
  * workgroups repeat that work), the classifier 2 / 8 waves 5021-5022 /
- * 5055-5057, layer 0's QKV 2 waves 5031-5035. */
+ * 5055-5057, layer 0's QKV 2 waves 5031-5035; W2 alone 1 / 2 / 8 waves
+ * 5094-5098 / 5111-5115 / 4894-4900 against 5050-5057 at 4, so W2 takes
+ * 2 (192 workgroups). */
 #ifndef VX_DEC_QKV_WAVES
 #define VX_DEC_QKV_WAVES 2
 #endif
@@ -268,7 +271,7 @@ constexpr int kNearChunk = 2;
 #define VX_DEC_SWIGLU_WAVES 4
 #endif
 #ifndef VX_DEC_RESID_WAVES
-#define VX_DEC_RESID_WAVES 4
+#define VX_DEC_RESID_WAVES 2
 #endif
 #ifndef VX_DEC_WO_WAVES
 #define VX_DEC_WO_WAVES 4
