@@ -253,17 +253,18 @@ constexpr int kNearChunk = 2;
 #endif
 /* Waves per workgroup of each GEMV: 4 (256 threads), but 2 for the QKV
  * GEMVs of layers 1-11 (576 workgroups of one row pair per wave) and for
- * W2. Config 4,
- * graph mode, interleaved on one box: QKV 4 / 2 / 1 waves 4928-4932 /
- * 4961 / 4965-4971 tok/s, and on another box 4 / 2 4994-5001 / 5019-5025;
- * [W1; W3] 2 / 8 waves 4887-4894 / 4773-4776 against 4994-5001 at 4; W2 and
- * Wo 2 / 8 waves 4742-4745 / 4787 against 4994-5001 and 4928-4932. Then
- * each alone, against 5055-5056 at 4: Wo 2 / 8 waves 4734-4745 / 5055-5057
- * (each Wo workgroup merges every column's attention partials, so more
- * workgroups repeat that work), the classifier 2 / 8 waves 5021-5022 /
- * 5055-5057, layer 0's QKV 2 waves 5031-5035; W2 alone 1 / 2 / 8 waves
- * 5094-5098 / 5111-5115 / 4894-4900 against 5050-5057 at 4, so W2 takes
- * 2 (192 workgroups). */
+ * W2 (192 workgroups). Config 4, graph mode, variants interleaved on one
+ * box (tok/s):
+ *   QKV 4 / 2 / 1 waves: 4928-4932 / 4961 / 4965-4971, and on another box
+ *     4 / 2: 4994-5001 / 5019-5025;
+ *   [W1; W3] 2 / 8 waves: 4887-4894 / 4773-4776 against 4994-5001 at 4;
+ *   W2 1 / 2 / 8 waves: 5094-5098 / 5111-5115 / 4894-4900 against
+ *     5050-5057 at 4;
+ *   Wo 2 / 8 waves: 4734-4745 / 5055-5057 against 5055-5056 at 4 (each Wo
+ *     workgroup merges every column's attention partials, so more
+ *     workgroups repeat that work);
+ *   the classifier 2 / 8 waves: 5021-5022 / 5055-5057, layer 0's QKV 2
+ *     waves: 5031-5035, against 5055-5056 at 4. */
 #ifndef VX_DEC_QKV_WAVES
 #define VX_DEC_QKV_WAVES 2
 #endif
