@@ -117,8 +117,9 @@ typedef struct vx_llama_i8_weights {
   const float *rope;      /* [seq_len, head_size / 2, 2] */
 } vx_llama_i8_weights;
 
-/* Capture the token step as hipGraphs (8 steps, and 1 for the remainder)
- * and replay them (else: stream launches, one by one). */
+/* Capture the token step as hipGraphs (8 steps, and 1 for the remainder;
+ * one pair for positions whose attention takes the small rounds, one for
+ * the rest) and replay them (else: stream launches, one by one). */
 #define VX_LLAMA_GRAPH 1
 
 /* Upload a model to GPU[topology_id - 500]; NULL (and a [Vx HIP] line) when
