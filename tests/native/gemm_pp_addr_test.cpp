@@ -16,6 +16,15 @@
 //    MFMA expects (the swizzles of the load and of the read undo each
 //    other), and every B operand read stays inside its plane;
 //  - the epilogue stores every C element once, inside C.
+// For the stream-K launch (grids of one to one and a half rounds of G
+// workgroups, G = 16 .. 304) it checks that every (tile, K stage) is run by
+// exactly one workgroup, each tail tile's two halves by a writer and a reader
+// on one XCD (reader = writer + 8) whose stage ranges meet at the split, the
+// reader continuing the writer's order; that each workgroup's own tile is
+// the one the one-tile launch gives its first-round workgroup and the tail
+// tiles of an XCD are that launch's second-round tiles on it; that every
+// tile is stored once; and that slots, flags and partial-sum offsets stay in
+// the workspace.
 // Prints "ok" when every check holds.
 
 #include "../../vx_amd/csrc/kernels/gemm_pp_layout.h"
@@ -216,6 +225,110 @@ static void walk(const Shape &s) {
   }
 }
 
+static void walk_sk(const Shape &s, int groups) {
+  const int tiles_m = (int)((s.m + pp::kTileM - 1) / pp::kTileM);
+  const int tiles_n = (int)((s.n + pp::kTileN - 1) / pp::kTileN);
+  const int tiles = tiles_m * tiles_n;
+  const int steps = (int)(s.k / pp::kStageK);
+  CHECK(pp::sk_fits(tiles, groups, steps), "%d tiles on %d groups refused", tiles, groups);
+  if (!pp::sk_fits(tiles, groups, steps)) {
+    return;
+  }
+  const int slots = tiles - groups;
+  CHECK(slots <= pp::kSkMaxSlots, "%d slots", slots);
+  std::vector<int> cover((size_t)tiles * steps, 0), stored((size_t)tiles, 0);
+  std::vector<int> writer_of((size_t)slots, -1), reader_of((size_t)slots, -1);
+  for (int w = 0; w < groups; ++w) {
+    const pp::SkUnits u = pp::sk_units(w, tiles_m, tiles_n, groups, steps);
+    // its own tile is the one-tile launch's first-round tile of w
+    const pp::Tile first = pp::tile_of(w, tiles, tiles_m, tiles_n);
+    const pp::Tile own = u.writer ? u.u1 : u.u0;
+    CHECK(own.tm == first.tm && own.tn == first.tn, "workgroup %d own tile", w);
+    CHECK(u.writer + u.reader == (u.slot >= 0 ? 1 : 0), "workgroup %d role", w);
+    CHECK(u.len0 >= 1 && u.len1 >= 0 && u.len0 + u.len1 < 2 * steps,
+          "workgroup %d lengths %d %d", w, u.len0, u.len1);
+    for (int st = 0; st < u.len0 + u.len1; ++st) {
+      int tm, tn, step;
+      pp::sk_stage(u, st, tm, tn, step);
+      CHECK(tm >= 0 && tm < tiles_m && tn >= 0 && tn < tiles_n && step >= 0 && step < steps,
+            "workgroup %d stage %d -> (%d, %d) step %d", w, st, tm, tn, step);
+      if (tm >= 0 && tm < tiles_m && tn >= 0 && tn < tiles_n && step >= 0 && step < steps) {
+        cover[((size_t)tm * tiles_n + tn) * steps + step]++;
+      }
+    }
+    // the tiles it stores: a reader both units, others its last unit
+    if (u.reader) {
+      stored[(size_t)u.u0.tm * tiles_n + u.u0.tn]++;
+    }
+    const pp::Tile last = u.len1 > 0 ? u.u1 : u.u0;
+    stored[(size_t)last.tm * tiles_n + last.tn]++;
+    if (u.slot >= 0) {
+      CHECK(u.slot < slots, "workgroup %d slot %d", w, u.slot);
+      if (u.slot < slots) {
+        (u.writer ? writer_of : reader_of)[(size_t)u.slot] = w;
+      }
+    }
+  }
+  for (int t = 0; t < tiles; ++t) {
+    CHECK(stored[(size_t)t] == 1, "tile %d stored %d times", t, stored[(size_t)t]);
+    for (int st = 0; st < steps; ++st) {
+      CHECK(cover[(size_t)t * steps + st] == 1, "tile %d stage %d run %d times", t, st,
+            cover[(size_t)t * steps + st]);
+    }
+    if (failures > 20) {
+      return;
+    }
+  }
+  std::vector<int> second_round((size_t)tiles, 0);
+  for (int p = groups; p < tiles; ++p) {
+    const pp::Tile t = pp::tile_of(p, tiles, tiles_m, tiles_n);
+    second_round[(size_t)t.tm * tiles_n + t.tn] = 1 + (p & 7);
+  }
+  for (int sl = 0; sl < slots; ++sl) {
+    const int wr = writer_of[(size_t)sl], rd = reader_of[(size_t)sl];
+    CHECK(wr >= 0 && rd == wr + 8 && (wr & 7) == (rd & 7), "slot %d: writer %d reader %d", sl,
+          wr, rd);
+    if (wr < 0 || rd < 0) {
+      continue;
+    }
+    const pp::SkUnits a = pp::sk_units(wr, tiles_m, tiles_n, groups, steps);
+    const pp::SkUnits b = pp::sk_units(rd, tiles_m, tiles_n, groups, steps);
+    CHECK(a.u0.tm == b.u1.tm && a.u0.tn == b.u1.tn, "slot %d: halves of two tiles", sl);
+    CHECK(a.len0 == b.begin1 && b.begin1 + b.len1 == steps, "slot %d: split %d / %d + %d", sl,
+          a.len0, b.begin1, b.len1);
+    CHECK(second_round[(size_t)a.u0.tm * tiles_n + a.u0.tn] == 1 + (wr & 7),
+          "slot %d: tail tile not the one-tile launch's second-round tile on XCD %d", sl,
+          wr & 7);
+    for (int wave = 0; wave < pp::kWaves; ++wave) {
+      CHECK(pp::sk_flag(sl, wave) < pp::kSkMaxSlots * pp::kWaves, "flag of slot %d", sl);
+    }
+    CHECK(pp::sk_slot_off(sl) + (int64_t)pp::kSkSlotFloats * 4 <= pp::sk_bytes(slots) &&
+              pp::sk_slot_off(sl) >= pp::kSkFlagBytes && pp::sk_slot_off(sl) % 256 == 0,
+          "slot %d at %lld", sl, (long long)pp::sk_slot_off(sl));
+  }
+}
+
+static void walk_sk_slot_layout() {
+  std::vector<int> seen((size_t)pp::kSkSlotFloats / 4, 0);
+  for (int wave = 0; wave < pp::kWaves; ++wave) {
+    for (int i = 0; i < pp::kTM; ++i) {
+      for (int jj = 0; jj < pp::kTN; ++jj) {
+        for (int lane = 0; lane < 64; ++lane) {
+          const uint32_t off = pp::sk_part_off(wave, i, jj, lane);
+          CHECK(off == pp::sk_part_off(wave, i, jj, 0) + 16u * lane, "lane stride");
+          CHECK(off % 16 == 0 && off + 16 <= (uint32_t)pp::kSkSlotFloats * 4, "part at %u", off);
+          if (off % 16 == 0 && off + 16 <= (uint32_t)pp::kSkSlotFloats * 4) {
+            seen[off / 16]++;
+          }
+        }
+      }
+    }
+  }
+  for (size_t u = 0; u < seen.size(); ++u) {
+    CHECK(seen[u] == 1, "partial unit %zu written %d times", u, seen[u]);
+  }
+}
+
 int main() {
   const Shape shapes[] = {
       {4096, 4096, 4096, 4096, 4096, 4096},
@@ -238,6 +351,31 @@ int main() {
       return 1;
     }
   }
+  walk_sk_slot_layout();
+  const struct {
+    Shape s;
+    int groups;
+  } sk_cases[] = {
+      {{8192, 3072, 768, 768, 3072, 3072}, 256},   // the reference's benchmark: 384 tiles
+      {{8192, 2304, 768, 768, 2304, 2304}, 256},   // 288 tiles: 32 of 128 pairs
+      {{8000, 3000, 288, 288, 3000, 3001}, 256},   // ragged, odd stage count (9)
+      {{4864, 6144, 512, 512, 6144, 6144}, 304},   // 456 tiles on 304 CUs
+      {{2048, 2560, 4096, 4096, 2560, 2560}, 64},  // 80 tiles on 64
+      {{1024, 1536, 256, 264, 1544, 1540}, 16},    // 24 tiles on 16, padded rows
+  };
+  for (const auto &c : sk_cases) {
+    walk_sk(c.s, c.groups);
+    if (failures) {
+      fprintf(stderr, "stream-K failed on %lldx%lldx%lld at %d groups\n", (long long)c.s.m,
+              (long long)c.s.n, (long long)c.s.k, c.groups);
+      return 1;
+    }
+  }
+  CHECK(!pp::sk_fits(256, 256, 24), "one round taken");
+  CHECK(!pp::sk_fits(392, 256, 24), "more than one and a half rounds taken");
+  CHECK(!pp::sk_fits(300, 256, 24), "tiles not a multiple of 8 taken");
+  CHECK(!pp::sk_fits(384, 256, 4), "too few stages taken");
+
   // The predicate refuses what the kernel cannot take.
   CHECK(!pp::shape_ok(257, 777, 96, 96, 777, 777), "N = 777 taken");
   CHECK(!pp::shape_ok(256, 256, 100, 104, 256, 256), "K = 100 taken");

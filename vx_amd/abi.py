@@ -47,10 +47,11 @@ HIP_CTRL_GEMV_KERNEL = CTRL_VENDOR_BASE + 6
 HIP_CTRL_FA_SPLITS = CTRL_VENDOR_BASE + 7
 HIP_CTRL_FA_WORKSPACES = CTRL_VENDOR_BASE + 8
 HIP_CTRL_STAGING_STATS = CTRL_VENDOR_BASE + 9
+HIP_CTRL_GEMM_WORKSPACES = CTRL_VENDOR_BASE + 10
 # Kernels the GEMV control opcode can force (0 = automatic choice).
 GEMV_AUTO, GEMV_ROWS, GEMV_DOT2_B4, GEMV_LDS = 0, 1, 2, 3
 # Kernels the GEMM control opcode can force (0 = automatic choice).
-GEMM_AUTO, GEMM_TILED, GEMM_MFMA_PP, GEMM_F32_MFMA = 0, 2, 8, 9
+GEMM_AUTO, GEMM_TILED, GEMM_MFMA_PP, GEMM_F32_MFMA, GEMM_MFMA_SK = 0, 2, 8, 9, 10
 
 
 def memref_tag(dtype: int, rank: int) -> int:

@@ -437,7 +437,9 @@ void stage(const void *data, int64_t rows, int64_t cols, int64_t row_stride,
                                 caller_stream));
 }
 
-bool run_gemm(const vx_gemm_plan &plan, Arena *arena = nullptr) {
+/* `no_alloc`: the no-alloc entry point's call, which takes no device memory
+ * beyond its scratch (so no stream-K workspace either). */
+bool run_gemm(const vx_gemm_plan &plan, Arena *arena = nullptr, bool no_alloc = false) {
   const size_t in_esz = vx_dtype_bytes(plan.dtype);
   const size_t out_esz = vx_dtype_bytes(plan.out_dtype);
   if (!in_esz || !out_esz) {
@@ -481,6 +483,9 @@ bool run_gemm(const vx_gemm_plan &plan, Arena *arena = nullptr) {
   g.a = a.ptr, g.b = b.ptr, g.c = c.ptr;
   g.lda = a.row_stride, g.ldb = b.row_stride, g.ldc = c.row_stride;
   g.stamp = next_stamp();
+  /* The stream-K launch keeps a workspace per stream: not for the no-alloc
+   * entry point, and not into a graph being captured. */
+  g.may_split = !no_alloc && arena == nullptr && !capturing();
 
   vxk::GemmKernel which = vxk::gemm_pick(g);
   const int forced = forced_gemm_kernel.load();
@@ -1148,7 +1153,7 @@ uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
     return 0;
   }
   if (!need) {
-    if (!run_gemm(plan, nullptr)) {
+    if (!run_gemm(plan, nullptr, true)) {
       fprintf(stderr, "[Vx HIP] %s: no GPU kernel takes this GEMM's types\n",
               op);
       return 0;
@@ -1172,7 +1177,7 @@ uint64_t vx_hip_dispatch_async_noalloc(const void *binary_payload,
   Arena arena;
   arena.base = sc->ptr;
   arena.size = kNoAllocScratchBytes;
-  if (!run_gemm(plan, &arena)) {
+  if (!run_gemm(plan, &arena, true)) {
     fprintf(stderr, "[Vx HIP] %s: no GPU kernel takes this GEMM's types\n", op);
     return 0;
   }
@@ -1331,6 +1336,7 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
 #define VX_HIP_CTRL_FA_SPLITS (VX_CTRL_VENDOR_BASE + 7)
 #define VX_HIP_CTRL_FA_WORKSPACES (VX_CTRL_VENDOR_BASE + 8)
 #define VX_HIP_CTRL_STAGING_STATS (VX_CTRL_VENDOR_BASE + 9)
+#define VX_HIP_CTRL_GEMM_WORKSPACES (VX_CTRL_VENDOR_BASE + 10)
 
 int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   switch (opcode) {
@@ -1388,11 +1394,13 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
   }
   case VX_HIP_CTRL_GEMM_KERNEL: {
     /* payload -> int32_t: 0 automatic, 2 tiled (exact k order), 8 MFMA
-     * ping-pong (16-bit inputs), 9 f32 on f32 MFMAs. A forced kernel applies
-     * where it takes the shape. */
+     * ping-pong (16-bit inputs), 9 f32 on f32 MFMAs, 10 the ping-pong tiles
+     * as a stream-K launch. A forced kernel applies where it takes the
+     * shape. */
     const int32_t *which = static_cast<const int32_t *>(payload);
     if (!which || !(*which == 0 || *which == vxk::GEMM_TILED ||
-                    *which == vxk::GEMM_MFMA_PP || *which == vxk::GEMM_F32_MFMA)) {
+                    *which == vxk::GEMM_MFMA_PP || *which == vxk::GEMM_F32_MFMA ||
+                    *which == vxk::GEMM_MFMA_SK)) {
       return 0;
     }
     forced_gemm_kernel.store(*which);
@@ -1486,6 +1494,19 @@ int32_t vx_plugin_control(uint32_t opcode, void *payload) {
     vxk::flash_attn_workspace_stats(&out[0], &out[1]);
     return 1;
   }
+  case VX_HIP_CTRL_GEMM_WORKSPACES: {
+    /* payload -> int64_t[4]: stream-K GEMM workspaces held (one per device
+     * and stream that ran such a launch), their bytes, stream-K launches so
+     * far, and the workgroups such a launch runs on the current device (its
+     * CU count). */
+    int64_t *out = static_cast<int64_t *>(payload);
+    if (!out || !hip_available()) {
+      return 0;
+    }
+    vxk::gemm_workspace_stats(&out[0], &out[1], &out[2]);
+    out[3] = vxk::device_cu_count();
+    return 1;
+  }
   case VX_HIP_CTRL_POOL_DRAIN:
     if (hip_available()) {
       wait_for_kernels("pool drain");
@@ -1514,13 +1535,15 @@ int64_t vx_plugin_tensor_map(int64_t base, int64_t rank, int64_t elem_bytes,
  * programs and host code already call (reference
  * runtime/cuda_dispatch.cpp:2030-2035); the HIP-named pair is the same.
  * Moving off a stream frees, in that stream's order, the flash-attention
- * split workspace the library kept for it, so a stream the caller then
+ * split workspace and the stream-K GEMM workspace the library kept for it,
+ * so a stream the caller then
  * destroys leaves nothing behind and a later stream at the same address
  * starts with none. A stream must stay alive while it is set. */
 void vx_hip_set_stream(void *stream) {
   const hipStream_t next = static_cast<hipStream_t>(stream);
   if (caller_stream && caller_stream != next) {
     vxk::flash_attn_release_stream(caller_stream);
+    vxk::gemm_release_stream(caller_stream);
   }
   caller_stream = next;
 }

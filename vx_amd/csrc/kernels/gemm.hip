@@ -11,7 +11,9 @@
  * the LDS and the load path work at the same time. Workgroups are renumbered
  * so the 32 consecutive tiles each XCD receives form a patch of C (4 tile
  * rows deep; 2 for a grid of at most one round), which keeps each XCD's A
- * and B panels in its own L2.
+ * and B panels in its own L2. Grids of one to one and a half rounds of the
+ * CUs take gemm_mfma_sk instead: the same tiles on one workgroup per CU, the
+ * second round's tiles cut along K between two workgroups (stream-K).
  *
  * gemm_tiled takes every supported type pair, any shape and row stride:
  * 64x64 tiles, 16-deep K stages through LDS, one multiply and one add per
@@ -31,6 +33,9 @@
 #include "../vx_kernels.h"
 #include "gemm_pp_layout.h"
 
+#include <atomic>
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 namespace vxk {
@@ -228,11 +233,69 @@ __device__ __forceinline__ void put4(void *c, int64_t at, f32x4 v, bool vec) {
   }
 }
 
+/* A wave's 8 x 4 accumulator blocks of the C tile at (m0, n0): each lane
+ * stores 4 consecutive columns of a row per block, 32 stores per wave. N is
+ * a multiple of 8 and the first column a multiple of 4, so the 4 are all
+ * inside C or all past N. With `through` (the host sets it only when C is
+ * aligned for the vector stores and 256 of its rows stay within 31 bits of
+ * byte offset), the stores go through a buffer descriptor based at the tile
+ * with the agent-coherent policy (sc1): written through to memory rather
+ * than left dirty in the XCD's L2 for the end of the kernel to write back.
+ * On grids of short K, where C's write-out is a large part of the launch,
+ * that measured 3% faster (8192 x 3072 x 768 and 4096 x 4096 x 768, f32
+ * out); at K = 4096 and 8192 it was within noise or 1% slower. */
+template <int kOut>
+__device__ __forceinline__ void store_c(void *C, int64_t M, int64_t N, int64_t ldc,
+                                        int64_t m0, int64_t n0, int wm, int wn, int l16,
+                                        int kc, const f32x4 (&acc)[pp::kTM][pp::kTN],
+                                        bool vec, bool through) {
+  constexpr int kEsz = kOut == VX_DTYPE_F32 ? 4 : 2;
+  if (through) {
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<char *>(C) + (m0 * ldc + n0) * kEsz, (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < pp::kTM; ++i) {
+#pragma unroll
+      for (int jj = 0; jj < pp::kTN; ++jj) {
+        const int r = pp::c_row(wm, i, l16), c = pp::c_col(wn, jj, kc);
+        if (m0 + r < M && n0 + c < N) {
+          const int at = (int)(((int64_t)r * ldc + c) * kEsz);
+          if constexpr (kOut == VX_DTYPE_F32) {
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][jj]), cr,
+                                                   at, 0, 16 /* sc1 */);
+          } else {
+            uint32_t h[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              h[e] = kOut == VX_DTYPE_BF16 ? f32_to_bf16(acc[i][jj][e])
+                                           : f32_to_f16(acc[i][jj][e]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)}, cr, at, 0, 16 /* sc1 */);
+          }
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < pp::kTM; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < pp::kTN; ++jj) {
+      const int64_t row = m0 + pp::c_row(wm, i, l16);
+      const int64_t col = n0 + pp::c_col(wn, jj, kc);
+      if (row < M && col < N) {
+        put4<kOut>(C, row * ldc + col, acc[i][jj], vec);
+      }
+    }
+  }
+}
+
 template <bool kBf16, int kOut>
 __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
     void *__restrict__ C, int64_t M, int64_t N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n,
+    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, int through,
     uint64_t *__restrict__ stamp) {
   constexpr int kNS = 4;
   /* Optional clock stamp (null in ordinary launches; the branch is uniform):
@@ -363,21 +426,310 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
     lds_barrier();
   }
 
-  /* Each lane stores 4 consecutive columns of a row per block: 32 stores
-   * per wave where 128 scalar ones were. N is a multiple of 8 and the first
-   * column a multiple of 4, so the 4 are all inside C or all past N. */
   const bool vec = (ldc & 3) == 0 &&
                    ((uintptr_t)C & (kOut == VX_DTYPE_F32 ? 15 : 7)) == 0;
+  store_c<kOut>(C, M, N, ldc, m0, n0, wm, wn, l16, kc, acc, vec, through != 0);
+  if (wm == 0) {
+    lds_barrier(); /* matches group 1's extra barrier before the loop */
+  }
+  if (stamp && blockIdx.x == 0 && t == 0) {
+    const uint64_t clk1 = __builtin_amdgcn_s_memtime();
+    const uint64_t rt1 = __builtin_amdgcn_s_memrealtime();
+    stamp[0] = clk0;
+    stamp[1] = rt0;
+    stamp[2] = clk1;
+    stamp[3] = rt1;
+  }
+}
+
+/* Stream-K variant of gemm_mfma_pp for grids of G < T <= 1.5 G tiles on G
+ * workgroups, one per CU (pp::sk_fits): the same ring, phases and MFMA
+ * order, with each workgroup walking one or two units of stages in one
+ * stream (the issue side runs into the second unit while the compute side
+ * finishes the first). A CU thus runs its own tile plus part of a second-
+ * round tile instead of two whole tiles in turn, while the one-tile launch
+ * leaves half the CUs idle in its second round. Unit assignment, the split
+ * point and the workspace layout are in gemm_pp_layout.h (sk_*).
+ *
+ * A second-round tile is cut at stage h of K between a writer and a reader
+ * workgroup on one XCD. The writer runs stages [0, h) first and leaves the
+ * sums in a workspace slot (agent-coherent stores, sc1), waits until they
+ * are written and sets one flag per wave to `seq`; then it runs its own
+ * tile. The reader runs its own tile, stores it without waiting, runs stages
+ * [h, steps) from zero, and at the end waits for the flag of the writer wave
+ * with its index (polled by lane 0, bounded), adds the writer's sums to its
+ * own and clears the flag for the next launch. No L2 write-back is needed:
+ * the sums never sit dirty in a non-coherent cache level. Each element of
+ * such a tile is (its stages [0, h) in order) + (its stages [h, steps) in
+ * order): deterministic, though not the one-tile launch's bits. (Continuing
+ * the writer's sums instead would keep those bits, but the reader must then
+ * load them into the accumulators that still hold its own tile, so it waits
+ * out its own tile's stores first: 5-9 us of stall that made it no faster.)
+ *
+ * The writer was dispatched before the reader, so it is resident or done; a
+ * poll that runs out (about 0.2 s) makes the reader store NaN over its tile
+ * instead of hanging. C goes out written through (store_c), since every
+ * tile of this launch ends in its last stretch. */
+constexpr int kSkPolls = 1 << 21;
+
+template <bool kBf16, int kOut>
+__global__ __launch_bounds__(512, 1) void gemm_mfma_sk(
+    const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+    void *__restrict__ C, int64_t M, int64_t N, int K, int64_t lda,
+    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, char *__restrict__ ws,
+    int seq, int through, uint64_t *__restrict__ stamp) {
+  constexpr int kNS = 4;
+  uint64_t clk0 = 0, rt0 = 0;
+  if (stamp && blockIdx.x == 0) {
+    clk0 = __builtin_amdgcn_s_memtime();
+    rt0 = __builtin_amdgcn_s_memrealtime();
+  }
+  constexpr int kLoads = pp::kLoads;
+  constexpr int kTM = pp::kTM;
+  constexpr int kTN = pp::kTN;
+  static_assert(kNS == pp::kSlots, "ring depth");
+  __shared__ u32x4 ring[kNS][2][kDUnits];
+
+  const int t = threadIdx.x;
+  const int steps = K / kDStageK;
+  const pp::SkUnits un =
+      pp::sk_units((int)blockIdx.x, tiles_m, tiles_n, (int)gridDim.x, steps);
+  const int slot = un.slot;
+  const bool writer = un.writer, reader = un.reader;
+  const int len0 = un.len0, len1 = un.len1, begin1 = un.begin1;
+  const int total = len0 + len1;
+  /* the units' tiles as plain integers (the reader's own tile is its unit
+   * 0; the tile stored last is unit 1's where there is one) */
+  const int tm0 = un.u0.tm, tn0 = un.u0.tn, tm1 = un.u1.tm, tn1 = un.u1.tn;
+  const int last_tm = len1 > 0 ? tm1 : tm0, last_tn = len1 > 0 ? tn1 : tn0;
+
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int lane = t & 63;
+
+  uint32_t a_off[kLoads], b_off[kLoads];
+#pragma unroll
+  for (int p = 0; p < kLoads; ++p) {
+    a_off[p] = pp::a_load_off(wave, p, lane, lda);
+    b_off[p] = pp::b_load_off(wave, p, lane, ldb);
+  }
+  const uint32_t ring_base =
+      (uint32_t)(uintptr_t)(VX_LDS void *)&ring[0][0][0];
+  /* Stage s of the workgroup's stream: stage s of unit 0, or stage
+   * begin1 + s - len0 of unit 1. */
+  auto issue = [&](int s, int slot_) {
+    int tm, tn, step;
+    pp::sk_stage(len0, begin1, tm0, tn0, tm1, tn1, s, tm, tn, step);
+    const int64_t a0 = pp::a_stage_base((int64_t)tm * kTileM, lda, step);
+    const int64_t b0 = pp::b_stage_base((int64_t)tn * kTileN, ldb, step);
+    const i32x4 ra = buffer_rsrc(A + a0, pp::a_stage_bytes(M, K, lda, a0));
+    const i32x4 rb = buffer_rsrc(B + b0, pp::b_stage_bytes(N, K, ldb, b0));
+#pragma unroll
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(ra, a_off[p], ring_base + pp::lds_a_dst(slot_, wave, p));
+    }
+#pragma unroll
+    for (int p = 0; p < kLoads; ++p) {
+      dma16(rb, b_off[p], ring_base + pp::lds_b_dst(slot_, wave, p));
+    }
+  };
+
+  f32x4 acc[kTM][kTN];
 #pragma unroll
   for (int i = 0; i < kTM; ++i) {
 #pragma unroll
-    for (int jj = 0; jj < kTN; ++jj) {
-      const int64_t row = m0 + pp::c_row(wm, i, l16);
-      const int64_t col = n0 + pp::c_col(wn, jj, kc);
-      if (row < M && col < N) {
-        put4<kOut>(C, row * ldc + col, acc[i][jj], vec);
+    for (int j = 0; j < kTN; ++j) {
+      acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+
+  const int wm = wave >> 2;
+  const int wn = wave & 3;
+  const int l16 = lane & 15;
+  const int kc = lane >> 4;
+
+  auto frags = [&](int slot_, u32x4 (&af)[kTM], u32x4 (&bfr)[kTN]) {
+    const u32x4 *la = ring[slot_][0];
+    const VX_LDS char *lb = (const VX_LDS char *)&ring[slot_][1][0];
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      af[i] = la[pp::lds_a_read(wm, i, l16, kc)];
+    }
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int at = pp::lds_b_read(wn, j, hh, l16, kc);
+        const u32x2 v = __builtin_bit_cast(
+            u32x2,
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((VX_LDS i16x4 *)(lb + at)));
+        bfr[j][2 * hh] = v[0];
+        bfr[j][2 * hh + 1] = v[1];
       }
     }
+  };
+
+  const bool vec = (ldc & 3) == 0 &&
+                   ((uintptr_t)C & (kOut == VX_DTYPE_F32 ? 15 : 7)) == 0;
+  auto store_tile = [&](int tm, int tn) {
+    store_c<kOut>(C, M, N, ldc, (int64_t)tm * kTileM, (int64_t)tn * kTileN, wm, wn, l16, kc,
+                  acc, vec, through != 0);
+  };
+
+  /* Between the units, per wave: the writer leaves the sums of its tail
+   * stages in its slice of the slot and sets its flag once they are written;
+   * the reader stores its own tile, without waiting for the stores. Both
+   * restart their accumulators from zero. The writer's partial-sum stores
+   * and the reader's tile stores take the same path through the code (the
+   * side that does not make them points its stores past the slot's range,
+   * where they are dropped, or skips the tile), so the accumulators take
+   * one path. */
+  constexpr uint32_t kPast = 0x80000000u; /* past every range */
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(ws + pp::sk_slot_off(slot < 0 ? 0 : slot)), (short)0, pp::kSkSlotFloats * 4,
+      0x00020000);
+  int *flag = reinterpret_cast<int *>(ws) + pp::sk_flag(slot < 0 ? 0 : slot, wave);
+  auto hand_over = [&]() {
+    if (reader) {
+      store_tile(tm0, tn0);
+    }
+    const int put_at = (int)(writer ? (uint32_t)lane * 16u : kPast);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int jj = 0; jj < kTN; ++jj) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][jj]), pr,
+                                               put_at, (int)pp::sk_part_off(wave, i, jj, 0),
+                                               16 /* sc1 */);
+        acc[i][jj] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+    if (writer) {
+      wait_vm<0>(); /* the slice is written before the flag says so */
+      if (lane == 0) {
+        __hip_atomic_store(flag, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  };
+  /* The reader, after its tail stages: waits for the writer wave's flag
+   * (polled by lane 0, bounded), adds the writer's sums to its own, a
+   * quarter of the blocks at a time with the next quarter's loads in flight,
+   * and clears the flag for the next launch. Each C element of a tail tile
+   * is thus (sum of stages [0, h)) + (sum of stages [h, steps)), each adding
+   * its stages in order. False when the wait ran out. */
+  auto take_partial = [&]() -> bool {
+    int got = seq;
+    if (lane == 0) {
+      for (int n = 0; n < kSkPolls; ++n) {
+        got = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (got == seq) {
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    const bool ok = __builtin_amdgcn_readfirstlane(got) == seq;
+    const int get_at = (int)(ok ? (uint32_t)lane * 16u : kPast);
+    constexpr int kQ = kTM / 4; /* rows of blocks per quarter */
+    f32x4 part[2][kQ][kTN];
+    auto fetch = [&](int q, f32x4 (&dst)[kQ][kTN]) {
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < kTN; ++jj) {
+          dst[i][jj] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         pr, get_at, (int)pp::sk_part_off(wave, q * kQ + i, jj, 0),
+                         16 /* sc1 */));
+        }
+      }
+    };
+    auto add = [&](int q, const f32x4 (&src)[kQ][kTN]) {
+#pragma unroll
+      for (int i = 0; i < kQ; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < kTN; ++jj) {
+          acc[q * kQ + i][jj] = src[i][jj] + acc[q * kQ + i][jj];
+        }
+      }
+    };
+    fetch(0, part[0]);
+    fetch(1, part[1]);
+    wait_vm<kQ * kTN>();
+    add(0, part[0]);
+    fetch(2, part[0]);
+    wait_vm<kQ * kTN>();
+    add(1, part[1]);
+    fetch(3, part[1]);
+    wait_vm<kQ * kTN>();
+    add(2, part[0]);
+    wait_vm<0>();
+    add(3, part[1]);
+    if (lane == 0) {
+      __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return ok;
+  };
+
+#pragma unroll
+  for (int s = 0; s < kNS - 1; ++s) {
+    if (s < total) {
+      issue(s, s);
+    }
+  }
+  wait_stages<kNS - 2, 2 * kLoads>(min(total - 1, kNS - 2));
+  lds_barrier();
+  if (wm == 1) {
+    lds_barrier();
+  }
+  /* One load phase and one compute phase; the issue side runs three stages
+   * ahead, across the boundary between the units. */
+  auto stage = [&](int j) {
+    u32x4 af[kTM], bfr[kTN];
+    if (j + kNS - 1 < total) {
+      issue(j + kNS - 1, (j + kNS - 1) % kNS);
+    }
+    frags(j % kNS, af, bfr);
+    if (j + 1 < total) {
+      wait_stages<kNS - 2, 2 * kLoads>(min(total - 2 - j, kNS - 2));
+    }
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int jj = 0; jj < kTN; ++jj) {
+#pragma unroll
+      for (int i0 = 0; i0 < kTM; ++i0) {
+        const int i = (jj & 1) ? kTM - 1 - i0 : i0;
+        acc[i][jj] = mfma16<kBf16>(bfr[jj], af[i], acc[i][jj]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  };
+  for (int j = 0; j < len0; ++j) {
+    stage(j);
+  }
+  bool ok = true;
+  if (len1 > 0) {
+    hand_over();
+    for (int j = len0; j < total; ++j) {
+      stage(j);
+    }
+    if (reader) {
+      ok = take_partial();
+    }
+  }
+  store_tile(last_tm, last_tn);
+  if (!ok) {
+    /* the writer's sums never came: the tile is marked as wrong */
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int jj = 0; jj < kTN; ++jj) {
+        acc[i][jj] = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                           __builtin_nanf("")};
+      }
+    }
+    store_tile(last_tm, last_tn);
   }
   if (wm == 0) {
     lds_barrier(); /* matches group 1's extra barrier before the loop */
@@ -699,14 +1051,28 @@ bool tiled_takes(const GemmArgs &g) {
   }
 }
 
+/* Whether store_c may write C through a tile-based buffer descriptor: C
+ * aligned for the vector stores and 256 rows of it within 31 bits of byte
+ * offset. */
+bool c_through_ok(const GemmArgs &g, int out) {
+  const int64_t esz = out == VX_DTYPE_F32 ? 4 : 2;
+  return (g.ldc & 3) == 0 && ((uintptr_t)g.c & (esz == 4 ? 15 : 7)) == 0 &&
+         (int64_t)kTileM * g.ldc * esz < (int64_t)INT32_MAX;
+}
+/* The one-tile launch writes C through for K up to this (measured faster at
+ * K = 768, the same or slower at 4096 and 8192); the stream-K launch, whose
+ * tiles all end in its last stretch, always does. */
+constexpr int64_t kThroughMaxK = 1536;
+
 template <bool kBf16, int kOut>
 void launch_pp(const GemmArgs &g, hipStream_t s) {
   const int tiles_m = (int)((g.m + kTileM - 1) / kTileM);
   const int tiles_n = (int)((g.n + kTileN - 1) / kTileN);
+  const int through = c_through_ok(g, kOut) && g.k <= kThroughMaxK;
   hipLaunchKernelGGL((gemm_mfma_pp<kBf16, kOut>), dim3(tiles_m * tiles_n),
                      dim3(512), 0, s, static_cast<const uint16_t *>(g.a),
                      static_cast<const uint16_t *>(g.b), g.c, g.m, g.n,
-                     (int)g.k, g.lda, g.ldb, g.ldc, tiles_m, tiles_n, g.stamp);
+                     (int)g.k, g.lda, g.ldb, g.ldc, tiles_m, tiles_n, through, g.stamp);
 }
 
 void launch_pp_any(const GemmArgs &g, hipStream_t s) {
@@ -718,6 +1084,93 @@ void launch_pp_any(const GemmArgs &g, hipStream_t s) {
   } else {
     launch_pp<false, VX_DTYPE_F16>(g, s);
   }
+}
+
+/* The stream-K launch takes what the ping-pong kernel takes when a workspace
+ * may be had (not under graph capture, not for the no-alloc entry point)
+ * and the grid is more than one round of the CUs but at most one and a half
+ * (pp::sk_fits). */
+bool sk_takes(const GemmArgs &g) {
+  if (!g.may_split || !pp_takes(g)) {
+    return false;
+  }
+  const int64_t tiles = ((g.m + kTileM - 1) / kTileM) * ((g.n + kTileN - 1) / kTileN);
+  const int cus = device_cu_count();
+  return tiles <= 2 * (int64_t)cus && (tiles - cus) <= pp::kSkMaxSlots &&
+         pp::sk_fits((int)tiles, cus, (int)(g.k / kDStageK));
+}
+
+/* Stream-K workspaces, one per (device, stream) like the flash-attention
+ * split workspace: launches on one stream run in order and share it; it
+ * grows (the old block freed in the stream's order) and is freed when the
+ * caller stream of a thread moves off it (gemm_release_stream). A fresh block
+ * has its flags zeroed; every reader clears the flag it consumed, and each
+ * launch marks its hand-overs with a new sequence number, so a flag left by
+ * an earlier launch never passes for this one's. */
+struct SkSpace {
+  char *base = nullptr;
+  size_t bytes = 0;
+  int seq = 0;
+};
+std::mutex sk_mutex;
+std::atomic<int64_t> sk_launches{0};
+std::map<std::pair<int, hipStream_t>, SkSpace> &sk_spaces() {
+  static auto *m = new std::map<std::pair<int, hipStream_t>, SkSpace>();
+  return *m;
+}
+
+bool sk_reserve(SkSpace &sp, size_t bytes, hipStream_t stream) {
+  if (sp.base && bytes <= sp.bytes) {
+    return true;
+  }
+  void *fresh = nullptr;
+  if (hipMallocAsync(&fresh, bytes, stream) != hipSuccess || !fresh) {
+    (void)hipGetLastError();
+    return false;
+  }
+  VX_HIP_CHECK(hipMemsetAsync(fresh, 0, (size_t)pp::kSkFlagBytes, stream));
+  if (sp.base) {
+    VX_HIP_CHECK(hipFreeAsync(sp.base, stream));
+  }
+  sp.base = static_cast<char *>(fresh);
+  sp.bytes = bytes;
+  return true;
+}
+
+template <bool kBf16, int kOut>
+void launch_sk(const GemmArgs &g, char *ws, int seq, hipStream_t s) {
+  const int tiles_m = (int)((g.m + kTileM - 1) / kTileM);
+  const int tiles_n = (int)((g.n + kTileN - 1) / kTileN);
+  hipLaunchKernelGGL((gemm_mfma_sk<kBf16, kOut>), dim3(device_cu_count()), dim3(512), 0,
+                     s, static_cast<const uint16_t *>(g.a),
+                     static_cast<const uint16_t *>(g.b), g.c, g.m, g.n, (int)g.k, g.lda,
+                     g.ldb, g.ldc, tiles_m, tiles_n, ws, seq, (int)c_through_ok(g, kOut),
+                     g.stamp);
+}
+
+/* False when no workspace could be had (the caller runs the ping-pong
+ * launch instead). */
+bool launch_sk_any(const GemmArgs &g, hipStream_t s) {
+  std::lock_guard<std::mutex> hold(sk_mutex);
+  int dev = 0;
+  VX_HIP_CHECK(hipGetDevice(&dev));
+  SkSpace &sp = sk_spaces()[{dev, s}];
+  const int64_t tiles = ((g.m + kTileM - 1) / kTileM) * ((g.n + kTileN - 1) / kTileN);
+  if (!sk_reserve(sp, (size_t)pp::sk_bytes((int)(tiles - device_cu_count())), s)) {
+    return false;
+  }
+  sp.seq = sp.seq == INT32_MAX ? 1 : sp.seq + 1;
+  const bool bf = g.in_dtype == VX_DTYPE_BF16;
+  if (g.out_dtype == VX_DTYPE_F32) {
+    bf ? launch_sk<true, VX_DTYPE_F32>(g, sp.base, sp.seq, s)
+       : launch_sk<false, VX_DTYPE_F32>(g, sp.base, sp.seq, s);
+  } else if (bf) {
+    launch_sk<true, VX_DTYPE_BF16>(g, sp.base, sp.seq, s);
+  } else {
+    launch_sk<false, VX_DTYPE_F16>(g, sp.base, sp.seq, s);
+  }
+  ++sk_launches;
+  return true;
 }
 
 template <int kIn, int kOut>
@@ -747,6 +1200,8 @@ bool gemm_kernel_takes(GemmKernel which, const GemmArgs &g) {
   switch (which) {
   case GEMM_MFMA_PP:
     return pp_takes(g);
+  case GEMM_MFMA_SK:
+    return sk_takes(g);
   case GEMM_F32_MFMA:
     return f32_mfma_takes(g);
   case GEMM_TILED:
@@ -761,7 +1216,7 @@ GemmKernel gemm_pick(const GemmArgs &g) {
    * padding costs more than it saves there. */
   const bool big = g.m >= 64 && g.n >= 64 && (double)g.m * g.n * g.k >= 16777216.0;
   if (big && pp_takes(g)) {
-    return GEMM_MFMA_PP;
+    return sk_takes(g) ? GEMM_MFMA_SK : GEMM_MFMA_PP;
   }
   /* f32: the exact-order kernel (bit-equal to the reference's host loop)
    * below 2^30 multiply-adds, the MFMA kernel above. */
@@ -782,6 +1237,13 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
       return false;
     }
     launch_pp_any(g, stream);
+  } else if (which == GEMM_MFMA_SK) {
+    if (!sk_takes(g)) {
+      return false;
+    }
+    if (!launch_sk_any(g, stream)) {
+      launch_pp_any(g, stream);
+    }
   } else if (which == GEMM_F32_MFMA) {
     if (!f32_mfma_takes(g)) {
       return false;
@@ -818,6 +1280,51 @@ bool gemm_launch_kernel(GemmKernel which, const GemmArgs &g,
 
 bool gemm_launch(const GemmArgs &g, hipStream_t stream) {
   return gemm_launch_kernel(gemm_pick(g), g, stream);
+}
+
+int gemm_release_stream(hipStream_t stream) {
+  if (!stream) {
+    return 0;
+  }
+  /* A capturing stream would record the free into its graph: its block
+   * stays until a later release finds it idle. */
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &status) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (status != hipStreamCaptureStatusNone) {
+    return 0;
+  }
+  std::lock_guard<std::mutex> hold(sk_mutex);
+  int freed = 0;
+  auto &m = sk_spaces();
+  for (auto it = m.begin(); it != m.end();) {
+    if (it->first.second != stream) {
+      ++it;
+      continue;
+    }
+    if (it->second.base) {
+      VX_HIP_CHECK(hipFreeAsync(it->second.base, stream));
+      ++freed;
+    }
+    it = m.erase(it);
+  }
+  return freed;
+}
+
+void gemm_workspace_stats(int64_t *blocks, int64_t *bytes, int64_t *launches) {
+  std::lock_guard<std::mutex> hold(sk_mutex);
+  int64_t n = 0, total = 0;
+  for (const auto &e : sk_spaces()) {
+    if (e.second.base) {
+      ++n;
+      total += (int64_t)e.second.bytes;
+    }
+  }
+  *blocks = n;
+  *bytes = total;
+  *launches = sk_launches.load();
 }
 
 namespace {

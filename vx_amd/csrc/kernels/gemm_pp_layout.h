@@ -1,9 +1,10 @@
 /*
- * gemm_pp_layout.h -- the address arithmetic of gemm_mfma_pp (gemm.hip),
- * written once for the kernel and for the CPU check that walks it
- * (tests/native/gemm_pp_addr_test.cpp): the launch order, the buffer-to-LDS
- * load offsets and buffer ranges of each K stage, the LDS slots those loads
- * fill, the LDS reads of the MFMA operands and the epilogue's C indices.
+ * gemm_pp_layout.h -- the address arithmetic of gemm_mfma_pp and its
+ * stream-K launch gemm_mfma_sk (gemm.hip), written once for the kernels and
+ * for the CPU check that walks it (tests/native/gemm_pp_addr_test.cpp): the
+ * launch order, the buffer-to-LDS load offsets and buffer ranges of each K
+ * stage, the LDS slots those loads fill, the LDS reads of the MFMA operands,
+ * the epilogue's C indices, and the stream-K units and workspace.
  * Plain C++ apart from the host/device qualifier, so g++ builds the check.
  */
 #ifndef VX_AMD_GEMM_PP_LAYOUT_H
@@ -59,14 +60,9 @@ struct Tile {
   int tm, tn;
 };
 
-/* The C tile workgroup `block` of `nwg` computes. Workgroup i runs on XCD
- * i % 8; the renumbering gives each XCD consecutive ids, which walk C in
- * groups of group_m tile rows, column by column. */
-VX_PP_FN Tile tile_of(int block, int nwg, int tiles_m, int tiles_n) {
-  int id = block;
-  if ((nwg & 7) == 0) {
-    id = (id & 7) * (nwg >> 3) + (id >> 3);
-  }
+/* The C tile at launch-order id `id`: ids walk C in groups of group_m tile
+ * rows, column by column. */
+VX_PP_FN Tile tile_at(int id, int tiles_m, int tiles_n) {
   const int group_m = tiles_m * tiles_n <= kSmallGrid ? kSmallGroupM : kGroupM;
   const int group_size = group_m * tiles_n;
   const int first_m = (id / group_size) * group_m;
@@ -74,6 +70,114 @@ VX_PP_FN Tile tile_of(int block, int nwg, int tiles_m, int tiles_n) {
       tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
   const int in_group = id % group_size;
   return Tile{first_m + in_group % rows_in_group, in_group / rows_in_group};
+}
+
+/* The C tile workgroup `block` of `nwg` computes. Workgroup i runs on XCD
+ * i % 8; the renumbering gives each XCD consecutive ids. */
+VX_PP_FN Tile tile_of(int block, int nwg, int tiles_m, int tiles_n) {
+  int id = block;
+  if ((nwg & 7) == 0) {
+    id = (id & 7) * (nwg >> 3) + (id >> 3);
+  }
+  return tile_at(id, tiles_m, tiles_n);
+}
+
+/* Stream-K launch (gemm_mfma_sk), for grids of more tiles than the G
+ * workgroups that fit the GPU at once (one per CU) but at most half again as
+ * many. Its G workgroups take the T tiles of the one-tile-per-workgroup
+ * launch: workgroup w computes the tile the first round's workgroup w would
+ * (sk_full_id), and the T - G tiles of the second round are each cut at half
+ * of K between two workgroups of one XCD, w and w + 8 with w / 8 even
+ * (dispatch puts workgroup i on XCD i % 8). The lower id, the writer, runs
+ * stages [0, h) of its tail tile first and leaves the sums in a workspace
+ * slot, then its own tile; the higher id, the reader, runs its own tile,
+ * then stages [h, steps) of the tail tile, and adds the writer's sums at the
+ * end. The reader waits only for a workgroup dispatched before it. */
+VX_PP_FN bool sk_fits(int tiles, int groups, int steps) {
+  return groups >= 16 && groups % 8 == 0 && tiles % 8 == 0 && tiles > groups &&
+         2 * (tiles - groups) <= groups && steps >= 8;
+}
+VX_PP_FN int sk_full_id(int w, int tiles) { return (w & 7) * (tiles >> 3) + (w >> 3); }
+/* The tail slot (0 .. T - G - 1) workgroup w shares, or -1. */
+VX_PP_FN int sk_slot(int w, int tiles, int groups) {
+  const int per_xcd = (tiles - groups) >> 3;
+  const int pair = w >> 4;
+  return pair < per_xcd ? (w & 7) * per_xcd + pair : -1;
+}
+VX_PP_FN int sk_tail_id(int slot, int tiles, int groups) {
+  const int per_xcd = (tiles - groups) >> 3;
+  return (slot / per_xcd) * (tiles >> 3) + (groups >> 3) + slot % per_xcd;
+}
+VX_PP_FN bool sk_reader(int w) { return ((w >> 3) & 1) != 0; }
+/* The split: the writer takes 5 stages past half, since the reader's part
+ * carries the hand-over and the final sum (about 10 us more fixed time per
+ * tile than the writer's, in a per-workgroup timeline of 8192 x 3072 x 768;
+ * splits at 1/2 and 2/3 left the reader or, at K = 4096, the writer last). */
+VX_PP_FN int sk_split(int steps) {
+  return steps / 2 + 5 < steps - 1 ? steps / 2 + 5 : steps - 1;
+}
+
+/* The stages workgroup w runs: unit 0 (len0 stages from stage 0 of tile
+ * u0), then unit 1 (len1 stages from stage begin1 of tile u1; none for a
+ * workgroup without a tail slot). */
+struct SkUnits {
+  Tile u0, u1;
+  int len0, begin1, len1;
+  int slot;
+  bool writer, reader;
+};
+VX_PP_FN SkUnits sk_units(int w, int tiles_m, int tiles_n, int groups, int steps) {
+  const int tiles = tiles_m * tiles_n;
+  SkUnits u;
+  u.slot = sk_slot(w, tiles, groups);
+  u.reader = u.slot >= 0 && sk_reader(w);
+  u.writer = u.slot >= 0 && !sk_reader(w);
+  const Tile own = tile_at(sk_full_id(w, tiles), tiles_m, tiles_n);
+  const Tile tail = u.slot >= 0 ? tile_at(sk_tail_id(u.slot, tiles, groups), tiles_m, tiles_n)
+                                : own;
+  const int h = sk_split(steps);
+  /* field by field: a select between whole structs can become an indexed
+   * load from a private copy, which the GPU compiler treats as per-lane */
+  u.u0.tm = u.writer ? tail.tm : own.tm;
+  u.u0.tn = u.writer ? tail.tn : own.tn;
+  u.u1.tm = u.writer ? own.tm : tail.tm;
+  u.u1.tn = u.writer ? own.tn : tail.tn;
+  u.len0 = u.writer ? h : steps;
+  u.begin1 = u.reader ? h : 0;
+  u.len1 = u.slot < 0 ? 0 : (u.reader ? steps - h : steps);
+  return u;
+}
+/* Tile and K stage of the workgroup's stage s (0 .. len0 + len1 - 1), from
+ * its units' fields (plain integers, so the GPU keeps them scalar). */
+VX_PP_FN void sk_stage(int len0, int begin1, int tm0, int tn0, int tm1, int tn1, int s,
+                       int &tm, int &tn, int &step) {
+  const bool second = s >= len0;
+  tm = second ? tm1 : tm0;
+  tn = second ? tn1 : tn0;
+  step = second ? begin1 + (s - len0) : s;
+}
+VX_PP_FN void sk_stage(const SkUnits &u, int s, int &tm, int &tn, int &step) {
+  sk_stage(u.len0, u.begin1, u.u0.tm, u.u0.tn, u.u1.tm, u.u1.tn, s, tm, tn, step);
+}
+
+/* The stream-K workspace: kSkMaxSlots x kWaves flags (ints) at its start,
+ * then each slot's partial sums, 256 x 256 floats laid out as [wave][i][jj]
+ * [lane] f32x4, so writer and reader waves of the same index move whole
+ * 1 KiB rows of their accumulators. */
+constexpr int kSkMaxSlots = 1024;
+constexpr int kSkSlotFloats = kTileM * kTileN;
+constexpr int64_t kSkFlagBytes = (int64_t)kSkMaxSlots * kWaves * 4;
+VX_PP_FN int64_t sk_bytes(int slots) {
+  return kSkFlagBytes + (int64_t)slots * kSkSlotFloats * 4;
+}
+VX_PP_FN int sk_flag(int slot, int wave) { return slot * kWaves + wave; }
+/* Byte offset, within slot `slot`'s partial sums, of the f32x4 that block
+ * (i, jj) of `wave` holds in `lane`. */
+VX_PP_FN uint32_t sk_part_off(int wave, int i, int jj, int lane) {
+  return (uint32_t)((((wave * kTM + i) * kTN + jj) * 64 + lane) * 16);
+}
+VX_PP_FN int64_t sk_slot_off(int slot) {
+  return kSkFlagBytes + (int64_t)slot * kSkSlotFloats * 4;
 }
 
 /* A's LDS plane is [256 rows][4 chunks of 8 k], chunk XORed with bits 1-2

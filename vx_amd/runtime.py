@@ -138,6 +138,15 @@ class DispatchLibrary:
         if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMM_KERNEL, ctypes.byref(v)):
             raise ValueError(f"no GEMM kernel {which}")
 
+    def gemm_workspaces(self) -> dict:
+        """Stream-K GEMM workspaces held (one per device and stream that ran
+        such a launch), their bytes, stream-K launches so far, and the
+        workgroups (CUs) such a launch runs."""
+        out = (ctypes.c_int64 * 4)()
+        if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMM_WORKSPACES, out):
+            raise RuntimeError("the library answered no stream-K statistics")
+        return dict(blocks=out[0], bytes=out[1], launches=out[2], groups=out[3])
+
     def force_gemv_kernel(self, which: int) -> None:
         v = ctypes.c_int32(which)
         if not self.lib.vx_plugin_control(abi.HIP_CTRL_GEMV_KERNEL, ctypes.byref(v)):
