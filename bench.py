@@ -142,6 +142,7 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
     dispatch = lib.lib.vx_plugin_dispatch_async
 
     before = lib.stats()
+    sk_before = lib.gemm_workspaces()["launches"]
     settled = [0]
 
     def one():
@@ -186,8 +187,14 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
     rt = (st[:, 3] - st[:, 1]).astype(np.float64)
     clock_mhz = float(clk.sum() / rt.sum() * 100.0) if rt.sum() > 0 else None
     after = lib.stats()
-    assert after["gemm_mfma"] - before["gemm_mfma"] == (runs + 1) * steps + warmup + settled[0], \
-        "GEMM did not take the MFMA path"
+    total = (runs + 1) * steps + warmup + settled[0]
+    assert after["gemm_mfma"] - before["gemm_mfma"] == total, "GEMM did not take the MFMA path"
+    # Which launch ran: the stream-K one (one workgroup per CU, second-round
+    # tiles cut along K) for grids of one to one and a half rounds of the CUs,
+    # else one 256x256 tile per workgroup.
+    sk = lib.gemm_workspaces()["launches"] - sk_before
+    assert sk in (0, total), "the launch kind changed between dispatches"
+    launch = "stream-K" if sk else "one tile per workgroup"
     c = dc.numpy()
     assert np.isfinite(c).all()
     for x in (da, db, dc):
@@ -199,7 +206,8 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
                 c_head=np.ascontiguousarray(c[:64]),
                 runs_us=spread([x * 1e3 / steps for x in region_ms]),
                 tflops_runs=spread([flops / (x / steps * 1e-3) / 1e12 for x in region_ms]),
-                steps_us=spread([x * 1e3 for x in step_ms]), clock_mhz=clock_mhz)
+                steps_us=spread([x * 1e3 for x in step_ms]), clock_mhz=clock_mhz,
+                launch=launch)
 
 
 def bench_gemm_f32(lib, timer, steps: int = 50, n: int = 512):
@@ -720,7 +728,8 @@ def main() -> int:
         g8 = bench_gemm(lib, timer, 10, 2, n=8192)
         extra["gemm_bf16_8192"] = dict(config="bf16 x bf16 -> f32 GEMM, M=N=K=8192", ms=g8["ms_per_step"],
                                        tflops=g8["tflops"], frac_of_peak=g8["tflops"] / PEAK_BF16_TFLOPS,
-                                       steps_us=g8["steps_us"], clock_mhz=g8["clock_mhz"])
+                                       steps_us=g8["steps_us"], clock_mhz=g8["clock_mhz"],
+                                       launch=g8["launch"])
         log(f"gemm 8192 {g8['tflops']:.1f} TFLOP/s")
         # the reference's own GEMM benchmark shape (benchmarks/gpu_gemm/run.sh:
         # 8192 x 3072 x 768 beside 4096^3; cuBLAS on an A100 214.2 TFLOP/s,
@@ -730,8 +739,8 @@ def main() -> int:
         extra["gemm_bf16_8192x3072x768"] = dict(
             config="bf16 x bf16 -> f32 GEMM, M=8192 N=3072 K=768", ms=gr["ms_per_step"],
             tflops=gr["tflops"], frac_of_peak=gr["tflops"] / PEAK_BF16_TFLOPS,
-            steps_us=gr["steps_us"], clock_mhz=gr["clock_mhz"])
-        log(f"gemm 8192x3072x768 {gr['tflops']:.1f} TFLOP/s")
+            steps_us=gr["steps_us"], clock_mhz=gr["clock_mhz"], launch=gr["launch"])
+        log(f"gemm 8192x3072x768 {gr['tflops']:.1f} TFLOP/s ({gr['launch']})")
         log("gemm f32 512^3 (config 1)")
         extra["gemm_f32_512"] = bench_gemm_f32(lib, timer)
         log(f"gemm f32 512: {extra['gemm_f32_512']['us']:.1f} us device, "
