@@ -466,9 +466,10 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
  * load them into the accumulators that still hold its own tile, so it waits
  * out its own tile's stores first: 5-9 us of stall that made it no faster.)
  *
- * The writer was dispatched before the reader, so it is resident or done; a
- * poll that runs out (about 0.2 s) makes the reader store NaN over its tile
- * instead of hanging. C goes out written through (store_c), since every
+ * The writer was dispatched before the reader, so it is resident or done
+ * and normally long finished; a poll that runs out (2^21 polls of an
+ * agent-scope load and a 128-clock sleep: seconds at most) makes the reader
+ * store NaN over its tile instead of hanging. C goes out written through (store_c), since every
  * tile of this launch ends in its last stretch. */
 constexpr int kSkPolls = 1 << 21;
 
