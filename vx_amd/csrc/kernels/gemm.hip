@@ -469,8 +469,8 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
  * The writer was dispatched before the reader, so it is resident or done
  * and normally long finished; a poll that runs out (2^21 polls of an
  * agent-scope load and a 128-clock sleep: seconds at most) makes the reader
- * store NaN over its tile instead of hanging. C goes out written through (store_c), since every
- * tile of this launch ends in its last stretch. */
+ * store NaN over its tile instead of hanging. C goes out written through
+ * (store_c), since every tile of this launch ends in its last stretch. */
 constexpr int kSkPolls = 1 << 21;
 
 template <bool kBf16, int kOut>
