@@ -295,3 +295,39 @@ def test_noalloc_entry_takes_the_one_tile_launch(hiplib, rng):
     finally:
         for x in (da, db, dc):
             x.free()
+
+
+def test_ragged_grids_choose_and_match(hiplib):
+    """Seeded ragged shapes around the stream-K range, on the automatic
+    choice: grids of more than one and at most one and a half rounds, with a
+    tile count that is a multiple of 8, take the stream-K launch and the rest
+    the one-tile launch; every result is deterministic and within the 1e-4
+    rule of the f64 product on sampled rows."""
+    g = groups(hiplib)
+    rng = np.random.default_rng(4242)
+    cases = []
+    while len(cases) < 8:
+        tn = int(rng.integers(2, 13))
+        tm = int(rng.integers(g // tn, (3 * g) // (2 * tn) + 3))
+        m = 256 * tm - int(rng.integers(0, 200))
+        n = 256 * tn - 8 * int(rng.integers(0, 20))
+        k = 32 * int(rng.integers(8, 40))
+        cases.append((m, n, k))
+    for m, n, k in cases:
+        tiles = ((m + 255) // 256) * ((n + 255) // 256)
+        expect_sk = g < tiles <= g + g // 2 and tiles % 8 == 0 and g % 8 == 0
+        announce(f"ragged {m}x{n}x{k}: {tiles} tiles on {g} CUs, stream-K {expect_sk}")
+        a, b, a16, b16 = operands(rng, m, n, k, abi.DTYPE_BF16)
+        da, db = DeviceArray.of(hiplib, a16, abi.DTYPE_BF16), DeviceArray.of(hiplib, b16, abi.DTYPE_BF16)
+        dc = DeviceArray(hiplib, (m, n), abi.DTYPE_F32)
+        try:
+            before = hiplib.gemm_workspaces()["launches"]
+            c1 = run(hiplib, da, db, dc, abi.DTYPE_BF16, abi.DTYPE_F32, abi.GEMM_AUTO)
+            c2 = run(hiplib, da, db, dc, abi.DTYPE_BF16, abi.DTYPE_F32, abi.GEMM_AUTO)
+            took = hiplib.gemm_workspaces()["launches"] - before
+            assert took == (2 if expect_sk else 0), (m, n, k, took)
+            assert np.array_equal(c1, c2), f"{m}x{n}x{k}: results differ from launch to launch"
+            against_f64(c1, a, b, abi.DTYPE_F32, f"{m}x{n}x{k} against f64")
+        finally:
+            for x in (da, db, dc):
+                x.free()
