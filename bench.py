@@ -190,7 +190,7 @@ def bench_gemm(lib, timer, steps: int, warmup: int, n: int = 4096, m: int | None
     total = (runs + 1) * steps + warmup + settled[0]
     assert after["gemm_mfma"] - before["gemm_mfma"] == total, "GEMM did not take the MFMA path"
     # Which launch ran: the stream-K one (one workgroup per CU, second-round
-    # tiles cut along K) for grids of one to one and a half rounds of the CUs,
+    # tiles cut along K) for grids ending in a partial round of at most half,
     # else one 256x256 tile per workgroup.
     sk = lib.gemm_workspaces()["launches"] - sk_before
     assert sk in (0, total), "the launch kind changed between dispatches"

@@ -201,11 +201,11 @@ int32_t vx_hip_image_param_count(const void *image, size_t image_size,
  * kind=matmul dispatch of vx_plugin_dispatch_async, with the same payload,
  * arguments and result, except that host operands and a host result buffer
  * are staged through a fixed 16 MiB array per GPU (in this library's code
- * object) instead of the staging pool. Grids of more than one and at most
- * one and a half rounds of 256x256 tiles over the CUs run here one tile per
- * workgroup, where vx_plugin_dispatch_async runs them as a stream-K launch
- * that needs a workspace: the results then agree to 1e-5 relative (one
- * bf16 unit for bf16 output), not bit for bit. Returns 1 when the GEMM was issued,
+ * object) instead of the staging pool. Grids of 256x256 tiles that end in
+ * a partial round of at most half the CUs run here one tile per workgroup,
+ * where vx_plugin_dispatch_async ends them with a stream-K launch that needs
+ * a workspace: the results then agree to 1e-5 relative (one bf16 unit for
+ * bf16 output), not bit for bit. Returns 1 when the GEMM was issued,
  * 0 (reason on stderr, nothing launched) for a region that is not a routed
  * GEMM, a result published through a slot (host memory the program frees),
  * staging beyond 16 MiB, or staging while the caller stream is capturing a

@@ -16,8 +16,9 @@
 //    MFMA expects (the swizzles of the load and of the read undo each
 //    other), and every B operand read stays inside its plane;
 //  - the epilogue stores every C element once, inside C.
-// For the stream-K launch (grids of one to one and a half rounds of G
-// workgroups, G = 16 .. 304) it checks that every (tile, K stage) is run by
+// For the stream-K launch (the last G + r tiles of grids of q G + r tiles,
+// 0 < r <= G / 2, after a one-tile launch of the first (q - 1) G; G = 16 ..
+// 304) it checks that every (tile, K stage) is run by
 // exactly one workgroup, each tail tile's two halves by a writer and a reader
 // on one XCD (reader = writer + 8) whose stage ranges meet at the split, the
 // reader continuing the writer's order; that each workgroup's own tile is
@@ -228,20 +229,40 @@ static void walk(const Shape &s) {
 static void walk_sk(const Shape &s, int groups) {
   const int tiles_m = (int)((s.m + pp::kTileM - 1) / pp::kTileM);
   const int tiles_n = (int)((s.n + pp::kTileN - 1) / pp::kTileN);
-  const int tiles = tiles_m * tiles_n;
+  const int all = tiles_m * tiles_n;
   const int steps = (int)(s.k / pp::kStageK);
-  CHECK(pp::sk_fits(tiles, groups, steps), "%d tiles on %d groups refused", tiles, groups);
-  if (!pp::sk_fits(tiles, groups, steps)) {
+  // The one-tile launch runs launch-order ids [0, base), the stream-K launch
+  // the last `tiles`.
+  const int base = pp::sk_base(all, groups, steps);
+  CHECK(base >= 0 && base % groups == 0, "%d tiles on %d groups refused", all, groups);
+  if (base < 0 || base % groups != 0) {
     return;
   }
+  const int tiles = all - base;
+  CHECK(pp::sk_fits(tiles, groups, steps), "%d stream-K tiles on %d groups", tiles, groups);
   const int slots = tiles - groups;
-  CHECK(slots <= pp::kSkMaxSlots, "%d slots", slots);
-  std::vector<int> cover((size_t)tiles * steps, 0), stored((size_t)tiles, 0);
+  CHECK(slots > 0 && slots <= pp::kSkMaxSlots, "%d slots", slots);
+  if (!pp::sk_fits(tiles, groups, steps) || slots <= 0 || slots > pp::kSkMaxSlots) {
+    return;
+  }
+  // The tile the one-tile launch of the stream-K share's ids gives its
+  // workgroup p (p in [0, tiles)).
+  auto launch_tile = [&](int p) {
+    return pp::tile_at(base + ((p & 7) * (tiles >> 3) + (p >> 3)), tiles_m, tiles_n);
+  };
+  std::vector<int> cover((size_t)all * steps, 0), stored((size_t)all, 0);
   std::vector<int> writer_of((size_t)slots, -1), reader_of((size_t)slots, -1);
+  for (int b = 0; b < base; ++b) {
+    const pp::Tile t = pp::tile_of(b, base, tiles_m, tiles_n);
+    for (int st = 0; st < steps; ++st) {
+      cover[((size_t)t.tm * tiles_n + t.tn) * steps + st]++;
+    }
+    stored[(size_t)t.tm * tiles_n + t.tn]++;
+  }
   for (int w = 0; w < groups; ++w) {
-    const pp::SkUnits u = pp::sk_units(w, tiles_m, tiles_n, groups, steps);
+    const pp::SkUnits u = pp::sk_units(w, tiles_m, tiles_n, base, tiles, groups, steps);
     // its own tile is the one-tile launch's first-round tile of w
-    const pp::Tile first = pp::tile_of(w, tiles, tiles_m, tiles_n);
+    const pp::Tile first = launch_tile(w);
     const pp::Tile own = u.writer ? u.u1 : u.u0;
     CHECK(own.tm == first.tm && own.tn == first.tn, "workgroup %d own tile", w);
     CHECK(u.writer + u.reader == (u.slot >= 0 ? 1 : 0), "workgroup %d role", w);
@@ -269,7 +290,7 @@ static void walk_sk(const Shape &s, int groups) {
       }
     }
   }
-  for (int t = 0; t < tiles; ++t) {
+  for (int t = 0; t < all; ++t) {
     CHECK(stored[(size_t)t] == 1, "tile %d stored %d times", t, stored[(size_t)t]);
     for (int st = 0; st < steps; ++st) {
       CHECK(cover[(size_t)t * steps + st] == 1, "tile %d stage %d run %d times", t, st,
@@ -279,9 +300,9 @@ static void walk_sk(const Shape &s, int groups) {
       return;
     }
   }
-  std::vector<int> second_round((size_t)tiles, 0);
+  std::vector<int> second_round((size_t)all, 0);
   for (int p = groups; p < tiles; ++p) {
-    const pp::Tile t = pp::tile_of(p, tiles, tiles_m, tiles_n);
+    const pp::Tile t = launch_tile(p);
     second_round[(size_t)t.tm * tiles_n + t.tn] = 1 + (p & 7);
   }
   for (int sl = 0; sl < slots; ++sl) {
@@ -291,8 +312,8 @@ static void walk_sk(const Shape &s, int groups) {
     if (wr < 0 || rd < 0) {
       continue;
     }
-    const pp::SkUnits a = pp::sk_units(wr, tiles_m, tiles_n, groups, steps);
-    const pp::SkUnits b = pp::sk_units(rd, tiles_m, tiles_n, groups, steps);
+    const pp::SkUnits a = pp::sk_units(wr, tiles_m, tiles_n, base, tiles, groups, steps);
+    const pp::SkUnits b = pp::sk_units(rd, tiles_m, tiles_n, base, tiles, groups, steps);
     CHECK(a.u0.tm == b.u1.tm && a.u0.tn == b.u1.tn, "slot %d: halves of two tiles", sl);
     CHECK(a.len0 == b.begin1 && b.begin1 + b.len1 == steps, "slot %d: split %d / %d + %d", sl,
           a.len0, b.begin1, b.len1);
@@ -362,6 +383,9 @@ int main() {
       {{4864, 6144, 512, 512, 6144, 6144}, 304},   // 456 tiles on 304 CUs
       {{2048, 2560, 4096, 4096, 2560, 2560}, 64},  // 80 tiles on 64
       {{1024, 1536, 256, 264, 1544, 1540}, 16},    // 24 tiles on 16, padded rows
+      {{12288, 3072, 768, 768, 3072, 3072}, 256},  // 576 tiles: one-tile round, then 320
+      {{7936, 8192, 512, 512, 8192, 8192}, 304},   // 992 tiles: two one-tile rounds, then 384
+      {{12100, 2800, 320, 320, 2800, 2803}, 256},  // ragged, 2 rounds + 40 (11 x 48 = 528)
   };
   for (const auto &c : sk_cases) {
     walk_sk(c.s, c.groups);
@@ -375,6 +399,12 @@ int main() {
   CHECK(!pp::sk_fits(392, 256, 24), "more than one and a half rounds taken");
   CHECK(!pp::sk_fits(300, 256, 24), "tiles not a multiple of 8 taken");
   CHECK(!pp::sk_fits(384, 256, 4), "too few stages taken");
+  CHECK(pp::sk_base(384, 256, 24) == 0 && pp::sk_base(640, 256, 24) == 256 &&
+            pp::sk_base(1152, 256, 24) == 768,
+        "stream-K share of multi-round grids");
+  CHECK(pp::sk_base(256, 256, 24) < 0 && pp::sk_base(512, 256, 24) < 0 &&
+            pp::sk_base(448, 256, 24) < 0 && pp::sk_base(300, 256, 24) < 0,
+        "grids without a stream-K tail taken");
 
   // The predicate refuses what the kernel cannot take.
   CHECK(!pp::shape_ok(257, 777, 96, 96, 777, 777), "N = 777 taken");

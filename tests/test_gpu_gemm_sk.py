@@ -1,6 +1,7 @@
-"""The stream-K launch of the ping-pong GEMM, for grids of one to one and a
-half rounds of the CUs (the reference's own GEMM benchmark shape, 8192 x
-3072 x 768, is 384 tiles on 256 CUs): every workgroup runs its own tile,
+"""The stream-K launch of the ping-pong GEMM, for grids whose tiles end in a
+partial round of at most half the CUs (the reference's own GEMM benchmark
+shape, 8192 x 3072 x 768, is 384 tiles on 256 CUs; grids of more rounds run
+the rounds before in a one-tile launch first): every workgroup runs its own tile,
 and the second round's tiles are cut at half of K between two workgroups,
 the second adding the first's sums to its own at the end. Results are
 checked for determinism (bit-equal from launch to launch), against the
@@ -85,16 +86,24 @@ def against_f64(bits, a, b, out_dt, what):
 def shapes(g: int):
     """(m, n, k) of grids the stream-K launch takes on g CUs: one and a half
     rounds (at g = 256 the reference's benchmark shape), an eighth of a
-    round past one (32 of 128 pairs), and ragged edges with an odd stage
-    count (9)."""
+    round past one (32 of 128 pairs), ragged edges with an odd stage count
+    (9), and two and a quarter rounds (a one-tile round, then stream-K)."""
     full = [(8192, 3072, 768)] if g == 256 else [(256 * (3 * g // 16), 2048, 768)]
     return full + [
         (256 * (9 * g // 64), 2048, 768),
         (256 * (3 * g // 16) - 100, 2040, 288),
+        (256 * (9 * g // 32), 2048, 768),
     ]
 
 
-@pytest.mark.parametrize("case", [0, 1, 2])
+def takes_stream_k(tiles: int, g: int) -> bool:
+    """The library's rule: tiles = q g + r with q >= 1, 0 < r <= g / 2 and
+    g + r a multiple of 8 (K of at least 8 stages)."""
+    q, r = divmod(tiles, g)
+    return g % 8 == 0 and q >= 1 and 0 < r <= g // 2 and (g + r) % 8 == 0
+
+
+@pytest.mark.parametrize("case", [0, 1, 2, 3])
 @pytest.mark.parametrize("dts", [(abi.DTYPE_BF16, abi.DTYPE_F32), (abi.DTYPE_BF16, abi.DTYPE_BF16),
                                  (abi.DTYPE_F16, abi.DTYPE_F32)])
 def test_stream_k_deterministic_and_close(hiplib, rng, case, dts):
@@ -299,8 +308,7 @@ def test_noalloc_entry_takes_the_one_tile_launch(hiplib, rng):
 
 def test_ragged_grids_choose_and_match(hiplib):
     """Seeded ragged shapes around the stream-K range, on the automatic
-    choice: grids of more than one and at most one and a half rounds, with a
-    tile count that is a multiple of 8, take the stream-K launch and the rest
+    choice: grids with a stream-K tail (takes_stream_k) take it and the rest
     the one-tile launch; every result is deterministic and within the 1e-4
     rule of the f64 product on sampled rows."""
     g = groups(hiplib)
@@ -315,7 +323,7 @@ def test_ragged_grids_choose_and_match(hiplib):
         cases.append((m, n, k))
     for m, n, k in cases:
         tiles = ((m + 255) // 256) * ((n + 255) // 256)
-        expect_sk = g < tiles <= g + g // 2 and tiles % 8 == 0 and g % 8 == 0
+        expect_sk = takes_stream_k(tiles, g)
         announce(f"ragged {m}x{n}x{k}: {tiles} tiles on {g} CUs, stream-K {expect_sk}")
         a, b, a16, b16 = operands(rng, m, n, k, abi.DTYPE_BF16)
         da, db = DeviceArray.of(hiplib, a16, abi.DTYPE_BF16), DeviceArray.of(hiplib, b16, abi.DTYPE_BF16)

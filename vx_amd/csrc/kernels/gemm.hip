@@ -11,9 +11,11 @@
  * the LDS and the load path work at the same time. Workgroups are renumbered
  * so the 32 consecutive tiles each XCD receives form a patch of C (4 tile
  * rows deep; 2 for a grid of at most one round), which keeps each XCD's A
- * and B panels in its own L2. Grids of one to one and a half rounds of the
- * CUs take gemm_mfma_sk instead: the same tiles on one workgroup per CU, the
- * second round's tiles cut along K between two workgroups (stream-K).
+ * and B panels in its own L2. Grids of q rounds of the CUs plus a partial
+ * round of at most half take gemm_mfma_sk for their last full round and the
+ * partial one (after a one-tile launch of the q - 1 rounds before): the same
+ * tiles on one workgroup per CU, the partial round's tiles cut along K
+ * between two workgroups (stream-K).
  *
  * gemm_tiled takes every supported type pair, any shape and row stride:
  * 64x64 tiles, 16-deep K stages through LDS, one multiply and one add per
@@ -442,8 +444,10 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_pp(
   }
 }
 
-/* Stream-K variant of gemm_mfma_pp for grids of G < T <= 1.5 G tiles on G
- * workgroups, one per CU (pp::sk_fits): the same ring, phases and MFMA
+/* Stream-K variant of gemm_mfma_pp for G < T <= 1.5 G tiles on G
+ * workgroups, one per CU (pp::sk_fits): a whole grid of one to one and a half
+ * rounds, or the last G + r tiles of a grid of q G + r (pp::sk_base, after a
+ * one-tile launch of the rest). The same ring, phases and MFMA
  * order, with each workgroup walking one or two units of stages in one
  * stream (the issue side runs into the second unit while the compute side
  * finishes the first). A CU thus runs its own tile plus part of a second-
@@ -477,7 +481,7 @@ template <bool kBf16, int kOut>
 __global__ __launch_bounds__(512, 1) void gemm_mfma_sk(
     const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
     void *__restrict__ C, int64_t M, int64_t N, int K, int64_t lda,
-    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, char *__restrict__ ws,
+    int64_t ldb, int64_t ldc, int tiles_m, int tiles_n, int id_base, char *__restrict__ ws,
     int seq, int through, uint64_t *__restrict__ stamp) {
   constexpr int kNS = 4;
   uint64_t clk0 = 0, rt0 = 0;
@@ -493,8 +497,8 @@ __global__ __launch_bounds__(512, 1) void gemm_mfma_sk(
 
   const int t = threadIdx.x;
   const int steps = K / kDStageK;
-  const pp::SkUnits un =
-      pp::sk_units((int)blockIdx.x, tiles_m, tiles_n, (int)gridDim.x, steps);
+  const pp::SkUnits un = pp::sk_units((int)blockIdx.x, tiles_m, tiles_n, id_base,
+                                      tiles_m * tiles_n - id_base, (int)gridDim.x, steps);
   const int slot = un.slot;
   const bool writer = un.writer, reader = un.reader;
   const int len0 = un.len0, len1 = un.len1, begin1 = un.begin1;
@@ -1089,16 +1093,16 @@ void launch_pp_any(const GemmArgs &g, hipStream_t s) {
 
 /* The stream-K launch takes what the ping-pong kernel takes when a workspace
  * may be had (not under graph capture, not for the no-alloc entry point)
- * and the grid is more than one round of the CUs but at most one and a half
- * (pp::sk_fits). */
+ * and the grid ends in a partial round of at most half the CUs
+ * (pp::sk_base). */
 bool sk_takes(const GemmArgs &g) {
   if (!g.may_split || !pp_takes(g)) {
     return false;
   }
   const int64_t tiles = ((g.m + kTileM - 1) / kTileM) * ((g.n + kTileN - 1) / kTileN);
   const int cus = device_cu_count();
-  return tiles <= 2 * (int64_t)cus && (tiles - cus) <= pp::kSkMaxSlots &&
-         pp::sk_fits((int)tiles, cus, (int)(g.k / kDStageK));
+  return cus / 2 <= pp::kSkMaxSlots &&
+         pp::sk_base((int)tiles, cus, (int)(g.k / kDStageK)) >= 0;
 }
 
 /* Stream-K workspaces, one per (device, stream) like the flash-attention
@@ -1138,15 +1142,27 @@ bool sk_reserve(SkSpace &sp, size_t bytes, hipStream_t stream) {
   return true;
 }
 
+/* A grid of q G + r tiles, q >= 2: the one-tile launch runs the first
+ * id_base = (q - 1) G launch-order ids (its workgroup renumbering is a
+ * bijection on them), then the stream-K launch the last G + r. */
 template <bool kBf16, int kOut>
 void launch_sk(const GemmArgs &g, char *ws, int seq, hipStream_t s) {
   const int tiles_m = (int)((g.m + kTileM - 1) / kTileM);
   const int tiles_n = (int)((g.n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((gemm_mfma_sk<kBf16, kOut>), dim3(device_cu_count()), dim3(512), 0,
-                     s, static_cast<const uint16_t *>(g.a),
+  const int cus = device_cu_count();
+  const int id_base = pp::sk_base(tiles_m * tiles_n, cus, (int)(g.k / kDStageK));
+  if (id_base > 0) {
+    const int through = c_through_ok(g, kOut) && g.k <= kThroughMaxK;
+    hipLaunchKernelGGL((gemm_mfma_pp<kBf16, kOut>), dim3(id_base), dim3(512), 0, s,
+                       static_cast<const uint16_t *>(g.a),
+                       static_cast<const uint16_t *>(g.b), g.c, g.m, g.n, (int)g.k, g.lda,
+                       g.ldb, g.ldc, tiles_m, tiles_n, through, (uint64_t *)nullptr);
+  }
+  hipLaunchKernelGGL((gemm_mfma_sk<kBf16, kOut>), dim3(cus), dim3(512), 0, s,
+                     static_cast<const uint16_t *>(g.a),
                      static_cast<const uint16_t *>(g.b), g.c, g.m, g.n, (int)g.k, g.lda,
-                     g.ldb, g.ldc, tiles_m, tiles_n, ws, seq, (int)c_through_ok(g, kOut),
-                     g.stamp);
+                     g.ldb, g.ldc, tiles_m, tiles_n, id_base, ws, seq,
+                     (int)c_through_ok(g, kOut), g.stamp);
 }
 
 /* False when no workspace could be had (the caller runs the ping-pong
@@ -1157,7 +1173,9 @@ bool launch_sk_any(const GemmArgs &g, hipStream_t s) {
   VX_HIP_CHECK(hipGetDevice(&dev));
   SkSpace &sp = sk_spaces()[{dev, s}];
   const int64_t tiles = ((g.m + kTileM - 1) / kTileM) * ((g.n + kTileN - 1) / kTileN);
-  if (!sk_reserve(sp, (size_t)pp::sk_bytes((int)(tiles - device_cu_count())), s)) {
+  const int cus = device_cu_count();
+  const int id_base = pp::sk_base((int)tiles, cus, (int)(g.k / kDStageK));
+  if (!sk_reserve(sp, (size_t)pp::sk_bytes((int)(tiles - id_base - cus)), s)) {
     return false;
   }
   sp.seq = sp.seq == INT32_MAX ? 1 : sp.seq + 1;

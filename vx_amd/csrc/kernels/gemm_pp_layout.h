@@ -97,6 +97,20 @@ VX_PP_FN bool sk_fits(int tiles, int groups, int steps) {
   return groups >= 16 && groups % 8 == 0 && tiles % 8 == 0 && tiles > groups &&
          2 * (tiles - groups) <= groups && steps >= 8;
 }
+/* For a grid of `all` tiles: the first launch-order id the stream-K launch
+ * takes (the one-tile launch runs the ids before it), or -1 when the grid
+ * has no such tail: `all` = q G + r with q >= 1 and 0 < r <= G / 2, and
+ * G + r taken by sk_fits. */
+VX_PP_FN int sk_base(int all, int groups, int steps) {
+  if (groups <= 0 || all <= groups) {
+    return -1;
+  }
+  const int q = all / groups, r = all - q * groups;
+  if (r == 0 || !sk_fits(groups + r, groups, steps)) {
+    return -1;
+  }
+  return (q - 1) * groups;
+}
 VX_PP_FN int sk_full_id(int w, int tiles) { return (w & 7) * (tiles >> 3) + (w >> 3); }
 /* The tail slot (0 .. T - G - 1) workgroup w shares, or -1. */
 VX_PP_FN int sk_slot(int w, int tiles, int groups) {
@@ -126,15 +140,19 @@ struct SkUnits {
   int slot;
   bool writer, reader;
 };
-VX_PP_FN SkUnits sk_units(int w, int tiles_m, int tiles_n, int groups, int steps) {
-  const int tiles = tiles_m * tiles_n;
+/* The stream-K launch takes the `tiles` launch-order ids from `id_base` on:
+ * all of a grid of one to one and a half rounds (id_base 0), or the last
+ * G + r ids of a grid of q G + r tiles, q >= 2, whose first (q - 1) G ids
+ * the one-tile launch runs before it (sk_base). */
+VX_PP_FN SkUnits sk_units(int w, int tiles_m, int tiles_n, int id_base, int tiles, int groups,
+                          int steps) {
   SkUnits u;
   u.slot = sk_slot(w, tiles, groups);
   u.reader = u.slot >= 0 && sk_reader(w);
   u.writer = u.slot >= 0 && !sk_reader(w);
-  const Tile own = tile_at(sk_full_id(w, tiles), tiles_m, tiles_n);
-  const Tile tail = u.slot >= 0 ? tile_at(sk_tail_id(u.slot, tiles, groups), tiles_m, tiles_n)
-                                : own;
+  const Tile own = tile_at(id_base + sk_full_id(w, tiles), tiles_m, tiles_n);
+  const Tile tail =
+      u.slot >= 0 ? tile_at(id_base + sk_tail_id(u.slot, tiles, groups), tiles_m, tiles_n) : own;
   const int h = sk_split(steps);
   /* field by field: a select between whole structs can become an indexed
    * load from a private copy, which the GPU compiler treats as per-lane */
