@@ -339,3 +339,69 @@ def test_ragged_grids_choose_and_match(hiplib):
         finally:
             for x in (da, db, dc):
                 x.free()
+
+
+def test_stream_k_from_threads(hiplib):
+    """Four host threads, each on its own stream (the caller stream is per
+    thread), alternate a one-and-a-half-round grid and a two-and-a-quarter-
+    round grid, so stream-K launches of several streams, each with its own
+    workspace, run at once and a reader can wait while other launches hold
+    CUs. The launch is deterministic, so every result must equal the one
+    the same call gives alone."""
+    import threading
+
+    g = groups(hiplib)
+    if g % 16:
+        pytest.skip(f"{g} CUs: no stream-K shape of whole 16ths")
+    announce("stream-K GEMMs from four threads on four streams")
+    rng = np.random.default_rng(99)
+    cases = []
+    for m, n, k in (shapes(g)[0], shapes(g)[3]):
+        _, _, a16, b16 = operands(rng, m, n, k, abi.DTYPE_BF16)
+        da, db = DeviceArray.of(hiplib, a16, abi.DTYPE_BF16), DeviceArray.of(hiplib, b16, abi.DTYPE_BF16)
+        dc = DeviceArray(hiplib, (m, n), abi.DTYPE_F32)
+        try:
+            want = run(hiplib, da, db, dc, abi.DTYPE_BF16, abi.DTYPE_F32, abi.GEMM_AUTO)
+        finally:
+            for x in (da, db, dc):
+                x.free()
+        cases.append((m, n, a16, b16, want))
+    launches = hiplib.gemm_workspaces()["launches"]
+    errors = []
+
+    def work(tid):
+        t = HipTimer()
+        s = t.stream_create()
+        arrays = []
+        try:
+            hiplib.lib.vx_hip_set_stream(s)
+            dev = []
+            for m, n, a16, b16, _ in cases:
+                xs = (DeviceArray.of(hiplib, a16, abi.DTYPE_BF16), DeviceArray.of(hiplib, b16, abi.DTYPE_BF16),
+                      DeviceArray(hiplib, (m, n), abi.DTYPE_F32))
+                arrays += list(xs)
+                dev.append(xs)
+            for it in range(4):
+                ci = (tid + it) % 2
+                da, db, dc = dev[ci]
+                matmul(hiplib, da.descriptor(), abi.DTYPE_BF16, db.descriptor(), abi.DTYPE_BF16,
+                       dc.descriptor(), abi.DTYPE_F32)
+                if not np.array_equal(dc.numpy().view(np.uint32), cases[ci][4]):
+                    errors.append((tid, it, "C differs from the launch alone"))
+        except Exception as e:  # reported below, with the thread that raised it
+            errors.append((tid, -1, repr(e)))
+        finally:
+            for x in arrays:
+                x.free()
+            hiplib.lib.vx_hip_set_stream(None)
+            t.sync()
+            t.stream_destroy(s)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=90)
+    assert not any(th.is_alive() for th in threads), "a launching thread did not finish"
+    assert not errors, errors
+    assert hiplib.gemm_workspaces()["launches"] == launches + 16
