@@ -739,7 +739,11 @@ def main() -> int:
         extra["gemm_bf16_8192x3072x768"] = dict(
             config="bf16 x bf16 -> f32 GEMM, M=8192 N=3072 K=768", ms=gr["ms_per_step"],
             tflops=gr["tflops"], frac_of_peak=gr["tflops"] / PEAK_BF16_TFLOPS,
-            steps_us=gr["steps_us"], clock_mhz=gr["clock_mhz"], launch=gr["launch"])
+            steps_us=gr["steps_us"], clock_mhz=gr["clock_mhz"], launch=gr["launch"],
+            # HBM-side bytes per launch from the committed counter profile of
+            # the stream-K launch (when that is the launch that ran)
+            traffic=(traffic_from_profiles("gemm_bf16_8192x3072x768_sk")
+                     if gr["launch"] == "stream-K" else None))
         log(f"gemm 8192x3072x768 {gr['tflops']:.1f} TFLOP/s ({gr['launch']})")
         log("gemm f32 512^3 (config 1)")
         extra["gemm_f32_512"] = bench_gemm_f32(lib, timer)
