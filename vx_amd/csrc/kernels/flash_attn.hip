@@ -520,6 +520,15 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
         scores(blk + 1, sn);
       }
       if (need_mask || scale_log2 < 0.0f) {
+        /* The lane's group g, read again from the lane id: the mask is its
+         * only use inside the key loop, and a value kept live across the
+         * loop for it was spilled (its reload waited for every load in
+         * flight). The asm keeps the compiler from hoisting it. */
+        int gm;
+        asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\t"
+                     "v_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                     "v_lshrrev_b32 %0, 5, %0"
+                     : "=v"(gm));
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt) {
           const int my_q = qw0 + 32 * qt + lq;
@@ -529,7 +538,7 @@ __global__ __launch_bounds__(kThreads, kQT == 1 ? 2 : 1) void flash_fwd(
           for (int kt = 0; kt < kKT; ++kt) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+              const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * gm + (r & 3);
               st[kt][qt][r] = key <= limit ? st[kt][qt][r] : hide;
             }
           }
